@@ -1,0 +1,80 @@
+#ifndef HD_GEMM_HIP_H
+#define HD_GEMM_HIP_H
+
+/*
+ * GEMM runtime of the MI355X engine: hand-written bf16 MFMA kernels for
+ * gfx950 (v_mfma_f32_32x32x16_bf16, fp32 accumulation, LDS double-buffered
+ * tiles filled by direct global->LDS loads, fused epilogues).
+ *
+ * Replaces the reference's src/cuda/gemm.h (lines 35-68). Same symbols and
+ * argument meaning. There is no vendor library behind hd_linear: the
+ * "runtime" holds the tile-configuration choice per shape and a persistent
+ * workspace for the caller, nothing else.
+ */
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "hidream_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct hd_gemm_runtime hd_gemm_runtime;
+
+/* gemm.h:35 - selects the device, allocates `workspace_bytes` of device
+ * memory for the caller, becomes the active runtime. NULL on failure. */
+hd_gemm_runtime *hd_gemm_runtime_init(int device_id, size_t workspace_bytes);
+/* gemm.h:38 */
+void hd_gemm_runtime_destroy(hd_gemm_runtime *rt);
+/* gemm.h:41-42 */
+void *hd_gemm_workspace(hd_gemm_runtime *rt);
+size_t hd_gemm_workspace_bytes(hd_gemm_runtime *rt);
+
+/* gemm.h:48 - simple one-output-per-thread fp32 kernel; correctness/debug
+ * backend. y[M,N] = x[M,K] . w[N,K]^T (+bias), bf16 out. */
+void hd_linear_reference(const void *x_dev, const void *w_dev,
+                         const void *bias_dev, void *y_dev,
+                         int M, int N, int K, int transpose_w);
+
+/* gemm.h:57 - production linear on the MFMA kernels (reference backend when
+ * hd_gemm_set_backend(0)). Only transpose_w == 1 ([out,in] weights). Bias is
+ * added in the epilogue with the production reference's two roundings,
+ * y = bf16(bf16(acc) + bias): the reference writes the bf16 GEMM result and
+ * then adds the bias in a second kernel (gemm.cu:226-235, :317-320). */
+void hd_linear(const void *x_dev, const void *w_dev, const void *bias_dev,
+               void *y_dev, int M, int N, int K, int transpose_w);
+
+/* gemm.h:61 - 1 = production (MFMA, default), 0 = reference kernel. */
+void hd_gemm_set_backend(int use_production);
+/* gemm.h:67 - accepted for source compatibility; there is one production
+ * kernel family, so the value is recorded and otherwise ignored. */
+void hd_gemm_set_prod_backend(int backend);
+
+/* ---- fused-epilogue entry points (extension) --------------------------
+ * y = bf16(res + bf16(x . W^T))      : residual epilogue (o_proj, down)   */
+void hd_linear_residual(const void *x_dev, const void *w_dev,
+                        const void *res_dev, void *y_dev, int M, int N, int K);
+
+/* y[M,F] = bf16(bf16(silu(bf16(x.Wg^T))) * bf16(x.Wu^T)) : gate/up GEMM
+ * with the SwiGLU epilogue; the gate and up products never reach HBM. */
+void hd_linear_swiglu(const void *x_dev, const void *wg_dev,
+                      const void *wu_dev, void *y_dev, int M, int F, int K);
+
+/* y[M, N0+N1+N2] = x . [W0;W1;W2]^T with three separately stored weight
+ * matrices (the q/k/v projections) computed as one GEMM; every Ni must be
+ * a multiple of 256. w1/w2 may be NULL (then N1/N2 must be 0). */
+void hd_linear_concat3(const void *x_dev, const void *w0, int N0,
+                       const void *w1, int N1, const void *w2, int N2,
+                       void *y_dev, int M, int K);
+
+/* Name of the kernel configuration hd_linear* would launch for a shape
+ * (diagnostics; static string). */
+const char *hd_gemm_config_name(int M, int N, int K, int epilogue);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HD_GEMM_HIP_H */

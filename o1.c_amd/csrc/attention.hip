@@ -1,0 +1,467 @@
+// Flash attention for gfx950 (head_dim 128, GQA, fp32 online softmax) and
+// the hd_sdpa_* plan API that replaces the reference's cuDNN-frontend SDPA
+// (src/cuda/hd_cudnn_sdpa.cu), plus the small eager attention used for
+// validation (attn.cu:22-173 semantics).
+//
+// Kernel layout (one wave = 32 query rows of one head, 4 waves per block):
+//  * S^T = K . Q^T with v_mfma_f32_32x32x16_bf16: the MFMA output puts one
+//    query per lane (lane % 32) and 16 key positions per lane, so the row
+//    max / row sum need a single xor-32 exchange;
+//  * O^T = V^T . P^T: the output accumulator also keeps one query per lane,
+//    so the online-softmax rescale is a per-lane scalar;
+//  * P^T feeds the second MFMA straight from the S^T registers. The key
+//    order inside each 16-key group that this implies (lane half h holds keys
+//    h*4..h*4+3 and 8+h*4..8+h*4+3) is matched by storing V^T with bits 2
+//    and 3 of the key index swapped ("vt" layout below), so every operand
+//    fetch is one 16-byte LDS read;
+//  * K and V^T tiles go global -> LDS with global_load_lds_dwordx4 into two
+//    buffers (64 keys per tile), XOR-swizzled by row.
+//
+// vt layout: [B, Hkv, 128, S_pad] bf16, S_pad = round_up(S, 64), key s
+// stored at column perm16(s) = s with bits 2 and 3 exchanged, padding zero.
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <math.h>
+
+#include "hd_common.hpp"
+#include "../../include/hd_hip.h"
+#include "../../include/hd_sdpa.h"
+
+#define FA_D 128
+#define FA_BQ 128      // queries per block (4 waves x 32)
+#define FA_BK 64       // keys per tile
+
+__host__ __device__ __forceinline__ int perm16(int s) {
+    return (s & ~12) | ((s & 4) << 1) | ((s & 8) >> 1);
+}
+static inline int64_t fa_spad(int64_t s) { return (s + FA_BK - 1) / FA_BK * FA_BK; }
+
+struct FaArgs {
+    const uint16_t *q;     // [B,Hq,S,D]
+    const uint16_t *k;     // [B,Hkv,S,D]
+    const uint16_t *vt;    // [B,Hkv,D,S_pad] (perm16 columns)
+    const uint16_t *mask;  // optional [S,S] additive bf16
+    uint16_t *out;         // seq-major [B,S,Hq*D] or head-major [B,Hq,S,D]
+    int S, S_pad, Hq, Hkv;
+    int ar_len;            // rows < ar_len: causal
+    int q_row_end;         // only rows < q_row_end are computed/written
+    float scale_log2;      // scale * log2(e)
+    int out_seq_major;
+};
+
+__device__ __forceinline__ void fa_wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <bool MASKED>
+__global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * (FA_BK * FA_D + FA_D * FA_BK)];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l32 = lane & 31, h = lane >> 5;
+
+    // block -> (b, head, q tile). Query heads sharing one kv head get
+    // consecutive linear ids so they run close together in time.
+    const int nqt = (a.q_row_end + FA_BQ - 1) / FA_BQ;
+    const int group = a.Hq / a.Hkv;
+    int lin = blockIdx.x;
+    const int g = lin % group; lin /= group;
+    const int qt = lin % nqt; lin /= nqt;
+    const int hk = lin % a.Hkv;
+    const int b = lin / a.Hkv;
+    const int hq = hk * group + g;
+
+    const int q0 = qt * FA_BQ + wave * 32;
+    const int my_q = q0 + l32;                       // this lane's query row
+    const bool causal_block = (qt * FA_BQ) < a.ar_len;
+    // keys needed by this block
+    int kv_end = a.S;
+    if (causal_block) {
+        int last_row = min(qt * FA_BQ + FA_BQ, a.q_row_end) - 1;
+        if (last_row < a.ar_len) kv_end = last_row + 1;
+    }
+    const int ntile = (kv_end + FA_BK - 1) / FA_BK;
+
+    // ---- Q fragments (B operand of S^T), held for the whole loop ---------
+    const uint16_t *qrow = a.q + (((size_t)b * a.Hq + hq) * a.S + min(my_q, a.S - 1)) * FA_D;
+    bf16x8_t qf[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) qf[ks] = *(const bf16x8_t *)(qrow + ks * 16 + h * 8);
+
+    // ---- loader addressing ------------------------------------------------
+    const uint16_t *kbase = a.k + ((size_t)b * a.Hkv + hk) * (size_t)a.S * FA_D;
+    const uint16_t *vbase = a.vt + ((size_t)b * a.Hkv + hk) * (size_t)FA_D * a.S_pad;
+    // K tile: 64 rows x 16 chunks; wave instr i covers rows 4*(wave*4+i) ..+4
+    // V^T tile: 128 rows x 8 chunks; wave instr i covers rows 8*(wave*4+i) ..+8
+    uint16_t *Ks0 = smem, *Vs0 = smem + 2 * FA_BK * FA_D;
+    auto issue = [&](int t, int buf) {
+        uint16_t *Ks = Ks0 + buf * FA_BK * FA_D, *Vs = Vs0 + buf * FA_D * FA_BK;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int row = (wave * 4 + i) * 4 + (lane >> 4);
+            int c = (lane & 15) ^ (row & 15);
+            int kv = min(t * FA_BK + row, a.S - 1);
+            __builtin_amdgcn_global_load_lds((const void *)(kbase + (size_t)kv * FA_D + c * 8),
+                                             (HD_LDS void *)(Ks + (wave * 4 + i) * 512), 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int row = (wave * 4 + i) * 8 + (lane >> 3);
+            int c = (lane & 7) ^ (row & 7);
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(vbase + (size_t)row * a.S_pad + t * FA_BK + c * 8),
+                (HD_LDS void *)(Vs + (wave * 4 + i) * 512), 16, 0, 0);
+        }
+    };
+
+    f32x16_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[i][r] = 0.f;
+    float m_run = -1e30f, l_run = 0.f;
+
+    issue(0, 0);
+    fa_wait_vm0();
+    __syncthreads();
+    for (int t = 0; t < ntile; t++) {
+        const int buf = t & 1;
+        if (t + 1 < ntile) issue(t + 1, buf ^ 1);
+        const uint16_t *Ks = Ks0 + buf * FA_BK * FA_D, *Vs = Vs0 + buf * FA_D * FA_BK;
+
+        // S^T for 64 keys: two 32-key tiles
+        f32x16_t s[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) s[j][r] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int row = j * 32 + l32;
+                const int c = ((ks * 2 + h) ^ (row & 15)) * 8;
+                bf16x8_t kf = *(const bf16x8_t *)(Ks + row * FA_D + c);
+                s[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[j], 0, 0, 0);
+            }
+        }
+
+        // scale, mask, tile max
+        const int kv0 = t * FA_BK;
+        float mt = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                float v = s[j][r] * a.scale_log2;
+                if (MASKED) {
+                    const int kv = kv0 + j * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+                    bool dead = kv >= a.S || (my_q < a.ar_len && kv > my_q);
+                    if (a.mask && !dead && my_q < a.S)
+                        v += bf2f(a.mask[(size_t)my_q * a.S + kv]) * 1.44269504088896341f;
+                    if (dead) v = -INFINITY;
+                }
+                s[j][r] = v;
+                mt = fmaxf(mt, v);
+            }
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = exp2f(m_run - m_new);
+        m_run = m_new;
+        float psum = 0.f;
+        bf16x8_t pf[4];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                uint32_t w[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float p0 = exp2f(s[j][hh * 8 + 2 * e] - m_new);
+                    float p1 = exp2f(s[j][hh * 8 + 2 * e + 1] - m_new);
+                    // row sum over the bf16-rounded probabilities the MFMA sees
+                    uint32_t pk = pack_bf2(p0, p1);
+                    psum += lo_bf(pk) + hi_bf(pk);
+                    w[e] = pk;
+                }
+                u32x4_t wv = {w[0], w[1], w[2], w[3]};
+                pf[j * 2 + hh] = __builtin_bit_cast(bf16x8_t, wv);
+            }
+        l_run = l_run * alpha + psum;
+        if (__builtin_amdgcn_read_exec() && alpha != 1.0f) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) o[i][r] *= alpha;
+        }
+        // O^T += V^T . P^T over 4 steps of 16 keys
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) {
+                const int row = dt * 32 + l32;
+                const int c = ((st * 2 + h) ^ (row & 7)) * 8;
+                bf16x8_t vf = *(const bf16x8_t *)(Vs + row * FA_BK + c);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[st], o[dt], 0, 0, 0);
+            }
+        }
+        fa_wait_vm0();
+        __syncthreads();
+    }
+
+    // ---- normalise and store ----------------------------------------------
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float inv = 1.0f / l_tot;
+    if (my_q >= a.q_row_end) return;
+    uint16_t *dst;
+    if (a.out_seq_major)
+        dst = a.out + (((size_t)b * a.S + my_q) * a.Hq + hq) * FA_D;
+    else
+        dst = a.out + (((size_t)b * a.Hq + hq) * a.S + my_q) * FA_D;
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int gq = 0; gq < 4; gq++) {
+            const int d = dt * 32 + gq * 8 + h * 4;
+            u32x2_t v = {pack_bf2(o[dt][gq * 4] * inv, o[dt][gq * 4 + 1] * inv),
+                         pack_bf2(o[dt][gq * 4 + 2] * inv, o[dt][gq * 4 + 3] * inv)};
+            *(u32x2_t *)(dst + d) = v;
+        }
+}
+
+// V [BH, S, D] -> vt [BH, D, S_pad] with perm16 columns and zero padding.
+__global__ __launch_bounds__(256) void fa_vt_kernel(const uint16_t *v, uint16_t *vt, int S,
+                                                    int S_pad) {
+    __shared__ uint16_t tile[64][FA_D + 2];
+    const int bh = blockIdx.y, s0 = blockIdx.x * 64;
+    const uint16_t *src = v + (size_t)bh * S * FA_D;
+    for (int i = threadIdx.x; i < 64 * FA_D; i += 256) {
+        int t = i / FA_D, d = i % FA_D;
+        tile[t][d] = (s0 + t < S) ? src[(size_t)(s0 + t) * FA_D + d] : (uint16_t)0;
+    }
+    __syncthreads();
+    uint16_t *dst = vt + (size_t)bh * FA_D * S_pad;
+    for (int i = threadIdx.x; i < 64 * FA_D; i += 256) {
+        int d = i / 64, p = i % 64;   // p: storage column within the tile
+        dst[(size_t)d * S_pad + s0 + p] = tile[perm16(p)][d];
+    }
+}
+
+extern "C" int64_t hd_flash_vt_bytes(int batch, int kv_heads, int seq) {
+    return (int64_t)batch * kv_heads * FA_D * fa_spad(seq) * 2;
+}
+
+// Writes the flash V^T layout from a head-major V (used by the plan API; the
+// decoder block's QKV epilogue writes it directly).
+extern "C" void hd_flash_make_vt(const void *v, void *vt, int bh, int seq) {
+    if (!v || !vt || bh <= 0 || seq <= 0) {
+        snprintf(hd_cuda_errbuf(), 512, "flash_make_vt: bad args");
+        return;
+    }
+    dim3 g(hd_cdiv(fa_spad(seq), 64), bh);
+    fa_vt_kernel<<<g, 256, 0, hd_stream()>>>((const uint16_t *)v, (uint16_t *)vt, seq,
+                                             (int)fa_spad(seq));
+    hd_check_launch("flash_make_vt");
+}
+
+static int fa_launch(const void *q, const void *k, const void *vt, const void *mask, void *out,
+                     int batch, int hq, int hkv, int seq, int ar_len, int q_row_end, float scale,
+                     int out_seq_major, hipStream_t st) {
+    FaArgs a;
+    a.q = (const uint16_t *)q;
+    a.k = (const uint16_t *)k;
+    a.vt = (const uint16_t *)vt;
+    a.mask = (const uint16_t *)mask;
+    a.out = (uint16_t *)out;
+    a.S = seq;
+    a.S_pad = (int)fa_spad(seq);
+    a.Hq = hq;
+    a.Hkv = hkv;
+    a.ar_len = ar_len;
+    a.q_row_end = q_row_end;
+    a.scale_log2 = scale * 1.44269504088896341f;
+    a.out_seq_major = out_seq_major;
+    const int nqt = (q_row_end + FA_BQ - 1) / FA_BQ;
+    dim3 grid((unsigned)((size_t)batch * hq * nqt));
+    bool masked = mask || ar_len > 0 || (seq % FA_BK) != 0;
+    if (masked) flash_fwd_kernel<true><<<grid, 256, 0, st>>>(a);
+    else flash_fwd_kernel<false><<<grid, 256, 0, st>>>(a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        snprintf(hd_cuda_errbuf(), 512, "hd_sdpa: flash launch failed: %s", hipGetErrorString(e));
+        return 1;
+    }
+    return 0;
+}
+
+extern "C" int hd_flash_attention(const void *q, const void *k, const void *vt, const void *mask,
+                                  void *out, int batch, int q_heads, int kv_heads, int seq,
+                                  int head_dim, int ar_len, float scale, int out_seq_major) {
+    if (!q || !k || !vt || !out || batch <= 0 || q_heads <= 0 || kv_heads <= 0 ||
+        q_heads % kv_heads || seq <= 0 || head_dim != FA_D || ar_len < 0 || ar_len > seq) {
+        snprintf(hd_cuda_errbuf(), 512, "hd_sdpa: flash bad args");
+        return 1;
+    }
+    return fa_launch(q, k, vt, mask, out, batch, q_heads, kv_heads, seq, ar_len, seq, scale,
+                     out_seq_major, hd_stream());
+}
+
+// ---------------------------------------------------------------------------
+// Plan API (hd_cudnn_sdpa.h). A plan is shape + split point + a V^T staging
+// buffer allocated once at create time (the reference allocates its cuDNN
+// workspace and causal staging there too, hd_cudnn_sdpa.cu:233-247, :354-368).
+// ---------------------------------------------------------------------------
+struct hd_sdpa_plan {
+    int B, Hq, Hkv, Sq, Skv, D;
+    int ar_len;
+    float scale;
+    void *vt;
+    size_t vt_bytes;
+};
+
+static int sdpa_err(const char *m) {
+    snprintf(hd_cuda_errbuf(), 512, "hd_sdpa: %s", m);
+    return 1;
+}
+
+static int plan_new(hd_sdpa_plan **out, int batch, int hq, int hkv, int sq, int skv, int d,
+                    int ar_len, float scale) {
+    if (!out) return sdpa_err("null out");
+    *out = nullptr;
+    if (batch < 1) return sdpa_err("invalid batch");
+    if (hq < 1 || hkv < 1 || hq % hkv) return sdpa_err("invalid head counts (q_heads % kv_heads != 0)");
+    if (sq < 1 || skv < 1 || d < 1) return sdpa_err("invalid dims");
+    if (d != FA_D) return sdpa_err("head_dim must be 128");
+    if (sq != skv) return sdpa_err("seq_q must equal seq_kv");
+    hd_sdpa_plan *p = new hd_sdpa_plan();
+    p->B = batch; p->Hq = hq; p->Hkv = hkv; p->Sq = sq; p->Skv = skv; p->D = d;
+    p->ar_len = ar_len;
+    p->scale = scale;
+    p->vt_bytes = (size_t)hd_flash_vt_bytes(batch, hkv, skv);
+    if (hipMalloc(&p->vt, p->vt_bytes) != hipSuccess) {
+        delete p;
+        return sdpa_err("hipMalloc V^T staging failed");
+    }
+    *out = p;
+    return 0;
+}
+
+extern "C" int hd_sdpa_create(hd_sdpa_plan **out, int batch, int q_heads, int kv_heads, int seq_q,
+                              int seq_kv, int head_dim, float scale) {
+    return plan_new(out, batch, q_heads, kv_heads, seq_q, seq_kv, head_dim, 0, scale);
+}
+
+extern "C" int hd_sdpa_create_split(hd_sdpa_plan **out, int batch, int q_heads, int kv_heads,
+                                    int seq, int ar_len, int head_dim, float scale) {
+    if (out) *out = nullptr;
+    if (ar_len < 0 || ar_len >= seq) return sdpa_err("invalid ar_len (must be 0 < ar_len < seq)");
+    return plan_new(out, batch, q_heads, kv_heads, seq, seq, head_dim, ar_len, scale);
+}
+
+extern "C" int hd_sdpa_create_prod(hd_sdpa_plan **out, int batch, int q_heads, int kv_heads,
+                                   int seq, int ar_len, int head_dim, float scale) {
+    if (!out) return sdpa_err("null out");
+    *out = nullptr;
+    if (ar_len > 0 && ar_len < seq)
+        return hd_sdpa_create_split(out, batch, q_heads, kv_heads, seq, ar_len, head_dim, scale);
+    return hd_sdpa_create(out, batch, q_heads, kv_heads, seq, seq, head_dim, scale);
+}
+
+extern "C" void hd_sdpa_destroy(hd_sdpa_plan *p) {
+    if (!p) return;
+    if (p->vt) (void)hipFree(p->vt);
+    delete p;
+}
+
+static int plan_run(hd_sdpa_plan *p, const void *q, const void *k, const void *v, const void *mask,
+                    void *out, void *stream, int ar_len, int q_row_end) {
+    hipStream_t st = stream ? (hipStream_t)stream : hd_stream();
+    dim3 g(hd_cdiv(fa_spad(p->Skv), 64), p->B * p->Hkv);
+    fa_vt_kernel<<<g, 256, 0, st>>>((const uint16_t *)v, (uint16_t *)p->vt, p->Skv,
+                                    (int)fa_spad(p->Skv));
+    if (hipGetLastError() != hipSuccess) return sdpa_err("V^T staging launch failed");
+    return fa_launch(q, k, p->vt, mask, out, p->B, p->Hq, p->Hkv, p->Sq, ar_len, q_row_end,
+                     p->scale, 0, st);
+}
+
+extern "C" int hd_sdpa_execute(hd_sdpa_plan *p, const void *q, const void *k, const void *v,
+                               const void *mask, void *out, void *stream) {
+    if (!p || !q || !k || !v || !out) return sdpa_err("null arg in execute");
+    if (p->ar_len > 0) return hd_sdpa_execute_split(p, q, k, v, out, stream);
+    return plan_run(p, q, k, v, mask, out, stream, 0, p->Sq);
+}
+
+extern "C" int hd_sdpa_execute_split(hd_sdpa_plan *p, const void *q, const void *k, const void *v,
+                                     void *out, void *stream) {
+    if (!p || !q || !k || !v || !out) return sdpa_err("null arg in execute");
+    if (p->ar_len <= 0) return sdpa_err("execute_split on a non-split plan");
+    return plan_run(p, q, k, v, nullptr, out, stream, p->ar_len, p->Sq);
+}
+
+extern "C" int hd_sdpa_execute_split_pass(hd_sdpa_plan *p, int which, const void *q, const void *k,
+                                          const void *v, void *out, void *stream) {
+    if (!p || !q || !k || !v || !out) return sdpa_err("null arg in execute");
+    if (p->ar_len <= 0) return sdpa_err("execute_split_pass on a non-split plan");
+    if (which == 0) return plan_run(p, q, k, v, nullptr, out, stream, p->ar_len, p->ar_len);
+    return plan_run(p, q, k, v, nullptr, out, stream, 0, p->Sq);
+}
+
+// ---------------------------------------------------------------------------
+// Eager attention (attn.cu:22-173 semantics) for small validation shapes:
+// fp32 scores, fp32 softmax, bf16 probs, fp32 P.V over bf16 probs,
+// seq-major output. Scores are recomputed instead of kept in an fp32
+// scratch, so nothing is allocated.
+// ---------------------------------------------------------------------------
+__global__ void eager_probs_kernel(const uint16_t *q, const uint16_t *k, const uint16_t *mask,
+                                   uint16_t *scores, uint16_t *probs, int H, int KV, int S, int D,
+                                   float scaling) {
+    int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= H * S) return;
+    int s = idx % S, hh = idx / S, kh = hh / (H / KV);
+    const uint16_t *qr = q + ((size_t)hh * S + s) * D;
+    auto score = [&](int t) {
+        const uint16_t *kr = k + ((size_t)kh * S + t) * D;
+        float acc = 0.f;
+        for (int d = 0; d < D; d++) acc += bf2f(qr[d]) * bf2f(kr[d]);
+        acc *= scaling;
+        return acc + bf2f(mask[(size_t)s * S + t]);
+    };
+    float mx = -INFINITY;
+    for (int t = 0; t < S; t++) mx = fmaxf(mx, score(t));
+    float sum = 0.f;
+    for (int t = 0; t < S; t++) sum += expf(score(t) - mx);
+    float inv = 1.0f / sum;
+    for (int t = 0; t < S; t++) {
+        float sc = score(t);
+        scores[((size_t)hh * S + s) * S + t] = f2bf(sc);
+        probs[((size_t)hh * S + s) * S + t] = f2bf(expf(sc - mx) * inv);
+    }
+}
+__global__ void eager_out_kernel(const uint16_t *probs, const uint16_t *v, uint16_t *out, int H,
+                                 int KV, int S, int D) {
+    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)H * S * D) return;
+    int d = idx % D;
+    size_t r = idx / D;
+    int hh = r % H, s = r / H, kh = hh / (H / KV);   // idx enumerates [S,H,D]
+    const uint16_t *pr = probs + ((size_t)hh * S + s) * S;
+    float acc = 0.f;
+    for (int t = 0; t < S; t++) acc += bf2f(pr[t]) * bf2f(v[((size_t)kh * S + t) * D + d]);
+    out[idx] = f2bf(acc);
+}
+extern "C" void hd_attention_eager(const void *q, const void *k, const void *v, const void *mask,
+                                   void *scores, void *probs, void *out, int heads, int kv_heads,
+                                   int seq, int dim, float scaling) {
+    if (!q || !k || !v || !mask || !scores || !probs || !out || heads <= 0 || kv_heads <= 0 ||
+        seq <= 0 || dim <= 0 || heads % kv_heads) {
+        snprintf(hd_cuda_errbuf(), 512, "attention_eager: bad args");
+        return;
+    }
+    eager_probs_kernel<<<hd_cdiv((size_t)heads * seq, 128), 128, 0, hd_stream()>>>(
+        (const uint16_t *)q, (const uint16_t *)k, (const uint16_t *)mask, (uint16_t *)scores,
+        (uint16_t *)probs, heads, kv_heads, seq, dim, scaling);
+    eager_out_kernel<<<hd_cdiv((size_t)heads * seq * dim, 256), 256, 0, hd_stream()>>>(
+        (const uint16_t *)probs, (const uint16_t *)v, (uint16_t *)out, heads, kv_heads, seq, dim);
+    hd_check_launch("attention_eager");
+}
+
+extern "C" int hd_sdpa_plan_ar_len(const hd_sdpa_plan *p) { return p ? p->ar_len : 0; }

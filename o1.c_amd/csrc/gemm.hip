@@ -1,0 +1,435 @@
+// bf16 GEMM for gfx950: C[M,N] = A[M,K] . B[N,K]^T, fp32 accumulation.
+//
+// Both operands are K-contiguous (activations [M,K], weights [out,in]).
+// Design (MI355X-first, not a translation of the reference's cuBLASLt use):
+//  * block tile BM x BN x 64, WGM x WGN waves, each wave a (BM/WGM) x
+//    (BN/WGN) sub-tile of 32x32 MFMA tiles (v_mfma_f32_32x32x16_bf16);
+//  * global -> LDS with global_load_lds_dwordx4 (no register staging), two
+//    LDS buffers, one barrier per K tile; 16-byte chunks XOR-swizzled by row
+//    so the ds_read_b128 fragment loads spread over the banks;
+//  * the MFMA is issued as weights x activations, so each lane ends with 4
+//    consecutive output columns of one output row per register group; the
+//    epilogue stages bf16 results through LDS and writes 16-byte coalesced
+//    rows, applying bias / residual there;
+//  * SwiGLU: a block's B tile holds gate rows and up rows of the same output
+//    columns, so gate and up land in the same lane and the epilogue forms
+//    bf16(bf16(silu(g)) * u) without either product reaching HBM;
+//  * blockIdx -> tile mapping is XCD-aware (the 8 XCDs get contiguous
+//    ranges of the grouped raster, so neighbouring tiles share an L2).
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <math.h>
+
+#include "hd_common.hpp"
+#include "../../include/hd_hip.h"
+#include "../../include/hd_gemm.h"
+
+enum { EPI_NONE = 0, EPI_BIAS = 1, EPI_RES = 2, EPI_SWIGLU = 3 };
+
+struct GemmArgs {
+    const uint16_t *A;       // [M, K]
+    const uint16_t *B[3];    // weight segments, each [rows, K]
+    int seg_end[3];          // exclusive end (in B-row space) of each segment
+    uint16_t *C;             // [M, ldc]
+    const uint16_t *bias;    // [N]
+    const uint16_t *res;     // [M, ldc]
+    int M, N, K;             // N = output columns
+    int ldc;
+    int ntm, ntn;            // tile grid
+};
+
+__device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <int BM, int BN, int WGM, int WGN, int EPI>
+struct GemmCfg {
+    static constexpr int NW = WGM * WGN;
+    static constexpr int NT = NW * 64;
+    static constexpr int WTM = BM / WGM, WTN = BN / WGN;
+    static constexpr int TM = WTM / 32, TN = WTN / 32;
+    static constexpr int WTN_OUT = EPI == EPI_SWIGLU ? WTN / 2 : WTN;
+    static constexpr int BN_OUT = EPI == EPI_SWIGLU ? BN / 2 : BN;
+    static constexpr int EPAD = 8;   // staging row padding (elements)
+    static constexpr int MAIN_BYTES = 2 * (BM + BN) * 64 * 2;
+    static constexpr int EPI_BYTES = NW * WTM * (WTN_OUT + EPAD) * 2;
+    static constexpr int LDS_BYTES = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
+    static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "loader split");
+    static_assert(TM >= 1 && TN >= 1, "wave tile");
+    static_assert(EPI != EPI_SWIGLU || TN % 2 == 0, "swiglu pairs");
+};
+
+__device__ __forceinline__ int xcd_remap(int b, int nb) {
+    const int per = nb / 8, rem = nb % 8;
+    const int xcd = b % 8, idx = b / 8;
+    return xcd * per + (xcd < rem ? xcd : rem) + idx;
+}
+
+template <int BM, int BN, int WGM, int WGN, int EPI>
+__global__ __launch_bounds__(WGM * WGN * 64) void gemm_bf16_kernel(GemmArgs g) {
+    using Cfg = GemmCfg<BM, BN, WGM, WGN, EPI>;
+    constexpr int NW = Cfg::NW, WTM = Cfg::WTM, WTN = Cfg::WTN, TM = Cfg::TM, TN = Cfg::TN;
+    constexpr int GROUP_M = 8;
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[Cfg::LDS_BYTES / 2];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+
+    // ---- tile coordinates: XCD-contiguous, grouped raster ----------------
+    const int nblk = g.ntm * g.ntn;
+    const int lin = xcd_remap(blockIdx.x, nblk);
+    const int in_group = GROUP_M * g.ntn;
+    const int first_m = (lin / in_group) * GROUP_M;
+    const int gm = min(g.ntm - first_m, GROUP_M);
+    const int tm = first_m + (lin % in_group) % gm;
+    const int tn = (lin % in_group) / gm;
+    const int m0 = tm * BM;
+
+    // ---- per-lane source rows of the loader (constant over K) ------------
+    constexpr int AI = BM / 8 / NW, BI = BN / 8 / NW;
+    const uint16_t *a_src[AI];
+    const uint16_t *b_src[BI];
+    const int sub = lane >> 3;                  // row within an 8-row group
+    const int chunk = (lane & 7) ^ sub;         // swizzled 16-byte chunk
+#pragma unroll
+    for (int i = 0; i < AI; i++) {
+        int r = (wave * AI + i) * 8 + sub;
+        int m = min(m0 + r, g.M - 1);
+        a_src[i] = g.A + (size_t)m * g.K + chunk * 8;
+    }
+#pragma unroll
+    for (int i = 0; i < BI; i++) {
+        int r = (wave * BI + i) * 8 + sub;
+        const uint16_t *p;
+        if (EPI == EPI_SWIGLU) {
+            int grp = r / WTN, j = r % WTN;
+            int n = tn * Cfg::BN_OUT + grp * (WTN / 2) + (j % (WTN / 2));
+            n = min(n, g.N - 1);
+            p = (j < WTN / 2 ? g.B[0] : g.B[1]) + (size_t)n * g.K;
+        } else {
+            int n = min(tn * BN + r, g.seg_end[2] - 1);
+            int s = n < g.seg_end[0] ? 0 : (n < g.seg_end[1] ? 1 : 2);
+            int base = s == 0 ? 0 : g.seg_end[s - 1];
+            p = g.B[s] + (size_t)(n - base) * g.K;
+        }
+        b_src[i] = p + chunk * 8;
+    }
+
+    uint16_t *As0 = smem, *Bs0 = smem + 2 * BM * 64;
+    auto issue = [&](int kt, int buf) {
+        uint16_t *As = As0 + buf * BM * 64, *Bs = Bs0 + buf * BN * 64;
+#pragma unroll
+        for (int i = 0; i < AI; i++)
+            __builtin_amdgcn_global_load_lds((const void *)(a_src[i] + kt * 64),
+                                             (HD_LDS void *)(As + (wave * AI + i) * 512), 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < BI; i++)
+            __builtin_amdgcn_global_load_lds((const void *)(b_src[i] + kt * 64),
+                                             (HD_LDS void *)(Bs + (wave * BI + i) * 512), 16, 0, 0);
+    };
+
+    f32x16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    const int nk = g.K / 64;
+    const int l32 = lane & 31, khalf = lane >> 5, sw = lane & 7;
+    issue(0, 0);
+    wait_vm0();
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) issue(kt + 1, buf ^ 1);
+        const uint16_t *As = As0 + buf * BM * 64, *Bs = Bs0 + buf * BN * 64;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const int c = ((ks * 2 + khalf) ^ sw) * 8;
+            bf16x8_t af[TM], bw[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                af[i] = *(const bf16x8_t *)(As + (wm * WTM + i * 32 + l32) * 64 + c);
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                bw[j] = *(const bf16x8_t *)(Bs + (wn * WTN + j * 32 + l32) * 64 + c);
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[j], af[i], acc[i][j], 0, 0, 0);
+        }
+        wait_vm0();
+        __syncthreads();
+    }
+
+    // ---- epilogue: stage bf16 through LDS, write coalesced rows ----------
+    constexpr int WO = Cfg::WTN_OUT, LDW = WO + Cfg::EPAD;
+    uint16_t *stg = smem + wave * WTM * LDW;
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        const int row = i * 32 + l32;
+#pragma unroll
+        for (int j = 0; j < (EPI == EPI_SWIGLU ? TN / 2 : TN); j++) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float x = acc[i][j][q * 4 + e];
+                    if (EPI == EPI_SWIGLU) {
+                        float gt = bfround(x);
+                        float up = bfround(acc[i][j + TN / 2][q * 4 + e]);
+                        float sg = bfround(gt * (1.0f / (1.0f + __expf(-gt))));
+                        x = sg * up;
+                    }
+                    v[e] = x;
+                }
+                const int col = j * 32 + q * 8 + khalf * 4;
+                u32x2_t pk = {pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+                *(u32x2_t *)(stg + row * LDW + col) = pk;
+            }
+        }
+    }
+    __syncthreads();
+    constexpr int CPR = WO / 8;              // 16-byte chunks per staged row
+    constexpr int RPI = 64 / CPR;            // rows per wave instruction
+    const int gm0 = m0 + wm * WTM;
+    const int gn0 = tn * Cfg::BN_OUT + wn * WO;
+#pragma unroll 4
+    for (int r0 = 0; r0 < WTM; r0 += RPI) {
+        const int r = r0 + lane / CPR, cc = (lane % CPR) * 8;
+        const int m = gm0 + r, n = gn0 + cc;
+        if (m < g.M && n < g.N) {
+            u32x4_t v = *(const u32x4_t *)(stg + r * LDW + cc);
+            if (EPI == EPI_BIAS || EPI == EPI_RES) {
+                u32x4_t o = EPI == EPI_BIAS ? *(const u32x4_t *)(g.bias + n)
+                                            : *(const u32x4_t *)(g.res + (size_t)m * g.ldc + n);
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    v[e] = pack_bf2(lo_bf(v[e]) + lo_bf(o[e]), hi_bf(v[e]) + hi_bf(o[e]));
+            }
+            *(u32x4_t *)(g.C + (size_t)m * g.ldc + n) = v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Reference kernel (gemm.cu:35-70 role): one fp32 dot product per output,
+// y = bf16(acc + bias). Correctness/debug backend and the fallback for
+// shapes the MFMA kernels do not take (K % 64, N % 8, misaligned).
+// ---------------------------------------------------------------------------
+__global__ void gemm_ref_kernel(const uint16_t *x, const uint16_t *w, const uint16_t *bias,
+                                uint16_t *y, int M, int N, int K) {
+    int n = blockIdx.x * 16 + (threadIdx.x & 15);
+    int m = blockIdx.y * 16 + (threadIdx.x >> 4);
+    if (m >= M || n >= N) return;
+    float acc = 0.f;
+    for (int k = 0; k < K; k++) acc += bf2f(x[(size_t)m * K + k]) * bf2f(w[(size_t)n * K + k]);
+    if (bias) acc += bf2f(bias[n]);
+    y[(size_t)m * N + n] = f2bf(acc);
+}
+
+__global__ void bias_add_kernel(const uint16_t *bias, uint16_t *y, int M, int N) {
+    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)M * N) return;
+    y[idx] = f2bf(bf2f(y[idx]) + bf2f(bias[idx % N]));
+}
+
+// ---------------------------------------------------------------------------
+// Runtime + dispatch
+// ---------------------------------------------------------------------------
+struct hd_gemm_runtime {
+    int device_id;
+    void *workspace;
+    size_t workspace_bytes;
+};
+static hd_gemm_runtime *g_rt = nullptr;
+static int g_use_production = 1;
+static int g_prod_backend = 0;
+
+extern "C" hd_gemm_runtime *hd_gemm_runtime_init(int device_id, size_t workspace_bytes) {
+    if (hipSetDevice(device_id) != hipSuccess) {
+        snprintf(hd_cuda_errbuf(), 512, "gemm rt: hipSetDevice(%d) failed", device_id);
+        return nullptr;
+    }
+    hd_gemm_runtime *rt = (hd_gemm_runtime *)calloc(1, sizeof(hd_gemm_runtime));
+    if (!rt) { snprintf(hd_cuda_errbuf(), 512, "gemm rt oom"); return nullptr; }
+    rt->device_id = device_id;
+    if (workspace_bytes) {
+        if (hipMalloc(&rt->workspace, workspace_bytes) != hipSuccess) {
+            snprintf(hd_cuda_errbuf(), 512, "gemm rt: workspace hipMalloc failed");
+            free(rt);
+            return nullptr;
+        }
+        rt->workspace_bytes = workspace_bytes;
+    }
+    g_rt = rt;
+    return rt;
+}
+extern "C" void hd_gemm_runtime_destroy(hd_gemm_runtime *rt) {
+    if (!rt) return;
+    if (rt->workspace) (void)hipFree(rt->workspace);
+    if (g_rt == rt) g_rt = nullptr;
+    free(rt);
+}
+extern "C" void *hd_gemm_workspace(hd_gemm_runtime *rt) { return rt ? rt->workspace : nullptr; }
+extern "C" size_t hd_gemm_workspace_bytes(hd_gemm_runtime *rt) { return rt ? rt->workspace_bytes : 0; }
+extern "C" void hd_gemm_set_backend(int p) { g_use_production = p; }
+extern "C" void hd_gemm_set_prod_backend(int b) { g_prod_backend = b; }
+
+template <int BM, int BN, int WGM, int WGN, int EPI>
+static void launch_cfg(GemmArgs &g) {
+    using Cfg = GemmCfg<BM, BN, WGM, WGN, EPI>;
+    g.ntm = (g.M + BM - 1) / BM;
+    g.ntn = (g.N + Cfg::BN_OUT - 1) / Cfg::BN_OUT;
+    gemm_bf16_kernel<BM, BN, WGM, WGN, EPI><<<g.ntm * g.ntn, Cfg::NT, 0, hd_stream()>>>(g);
+}
+
+// Tile configuration per shape. "big" (256x256, 4 waves of 128x128) when the
+// grid holds enough tiles to fill 256 CUs, else 128x128 tiles.
+template <int EPI>
+static const char *pick_and_launch(GemmArgs &g, bool launch) {
+    const int bn_out_big = EPI == EPI_SWIGLU ? 128 : 256;
+    long tiles_big = (long)((g.M + 255) / 256) * ((g.N + bn_out_big - 1) / bn_out_big);
+    if (tiles_big >= 256) {
+        if (launch) launch_cfg<256, 256, 2, 2, EPI>(g);
+        return "bf16_256x256x64_w2x2";
+    }
+    if (launch) launch_cfg<128, 128, 2, 2, EPI>(g);
+    return "bf16_128x128x64_w2x2";
+}
+
+static bool mfma_ok(const void *x, const void *y, int N, int K) {
+    return K % 64 == 0 && N % 8 == 0 && ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0);
+}
+
+static void gemm_launch(int epi, GemmArgs &g) {
+    switch (epi) {
+    case EPI_NONE: pick_and_launch<EPI_NONE>(g, true); break;
+    case EPI_BIAS: pick_and_launch<EPI_BIAS>(g, true); break;
+    case EPI_RES: pick_and_launch<EPI_RES>(g, true); break;
+    case EPI_SWIGLU: pick_and_launch<EPI_SWIGLU>(g, true); break;
+    }
+}
+
+extern "C" const char *hd_gemm_config_name(int M, int N, int K, int epi) {
+    GemmArgs g = {};
+    g.M = M; g.N = N; g.K = K;
+    if (K % 64 || N % 8) return "reference";
+    switch (epi) {
+    case EPI_BIAS: return pick_and_launch<EPI_BIAS>(g, false);
+    case EPI_RES: return pick_and_launch<EPI_RES>(g, false);
+    case EPI_SWIGLU: return pick_and_launch<EPI_SWIGLU>(g, false);
+    default: return pick_and_launch<EPI_NONE>(g, false);
+    }
+}
+
+extern "C" void hd_linear_reference(const void *x, const void *w, const void *bias, void *y,
+                                    int M, int N, int K, int transpose_w) {
+    if (!x || !w || !y || M <= 0 || N <= 0 || K <= 0) {
+        snprintf(hd_cuda_errbuf(), 512, "linear: bad args");
+        return;
+    }
+    if (!transpose_w) {
+        snprintf(hd_cuda_errbuf(), 512, "linear: transpose_w=0 unsupported");
+        return;
+    }
+    dim3 grid(hd_cdiv(N, 16), hd_cdiv(M, 16));
+    gemm_ref_kernel<<<grid, 256, 0, hd_stream()>>>((const uint16_t *)x, (const uint16_t *)w,
+                                                   (const uint16_t *)bias, (uint16_t *)y, M, N, K);
+    hd_check_launch("linear_reference");
+}
+
+extern "C" void hd_linear(const void *x, const void *w, const void *bias, void *y, int M, int N,
+                          int K, int transpose_w) {
+    if (!x || !w || !y || M <= 0 || N <= 0 || K <= 0) {
+        snprintf(hd_cuda_errbuf(), 512, "linear: bad args");
+        return;
+    }
+    if (!transpose_w) {
+        snprintf(hd_cuda_errbuf(), 512, "linear: transpose_w=0 unsupported");
+        return;
+    }
+    if (!g_use_production || !mfma_ok(x, y, N, K) || (bias && (uintptr_t)bias % 16)) {
+        // reference backend: fp32 result + bias rounded once; production
+        // rounding (two roundings) is kept by adding the bias separately.
+        hd_linear_reference(x, w, nullptr, y, M, N, K, 1);
+        if (bias) {
+            bias_add_kernel<<<hd_cdiv((size_t)M * N, 256), 256, 0, hd_stream()>>>(
+                (const uint16_t *)bias, (uint16_t *)y, M, N);
+            hd_check_launch("linear bias");
+        }
+        return;
+    }
+    GemmArgs g = {};
+    g.A = (const uint16_t *)x;
+    g.B[0] = g.B[1] = g.B[2] = (const uint16_t *)w;
+    g.seg_end[0] = g.seg_end[1] = g.seg_end[2] = N;
+    g.C = (uint16_t *)y;
+    g.bias = (const uint16_t *)bias;
+    g.M = M; g.N = N; g.K = K; g.ldc = N;
+    gemm_launch(bias ? EPI_BIAS : EPI_NONE, g);
+    hd_check_launch("linear");
+}
+
+extern "C" void hd_linear_residual(const void *x, const void *w, const void *res, void *y, int M,
+                                   int N, int K) {
+    if (!x || !w || !res || !y || M <= 0 || N <= 0 || K <= 0 || !mfma_ok(x, y, N, K) ||
+        (uintptr_t)res % 16) {
+        snprintf(hd_cuda_errbuf(), 512, "linear_residual: bad args");
+        return;
+    }
+    GemmArgs g = {};
+    g.A = (const uint16_t *)x;
+    g.B[0] = g.B[1] = g.B[2] = (const uint16_t *)w;
+    g.seg_end[0] = g.seg_end[1] = g.seg_end[2] = N;
+    g.C = (uint16_t *)y;
+    g.res = (const uint16_t *)res;
+    g.M = M; g.N = N; g.K = K; g.ldc = N;
+    gemm_launch(EPI_RES, g);
+    hd_check_launch("linear_residual");
+}
+
+extern "C" void hd_linear_swiglu(const void *x, const void *wg, const void *wu, void *y, int M,
+                                 int F, int K) {
+    if (!x || !wg || !wu || !y || M <= 0 || F <= 0 || K <= 0 || !mfma_ok(x, y, F, K) ||
+        F % 64) {
+        snprintf(hd_cuda_errbuf(), 512, "linear_swiglu: bad args");
+        return;
+    }
+    GemmArgs g = {};
+    g.A = (const uint16_t *)x;
+    g.B[0] = (const uint16_t *)wg;
+    g.B[1] = (const uint16_t *)wu;
+    g.B[2] = nullptr;
+    g.seg_end[0] = g.seg_end[1] = g.seg_end[2] = F;
+    g.C = (uint16_t *)y;
+    g.M = M; g.N = F; g.K = K; g.ldc = F;
+    gemm_launch(EPI_SWIGLU, g);
+    hd_check_launch("linear_swiglu");
+}
+
+extern "C" void hd_linear_concat3(const void *x, const void *w0, int N0, const void *w1, int N1,
+                                  const void *w2, int N2, void *y, int M, int K) {
+    int N = N0 + N1 + N2;
+    if (!x || !w0 || !y || M <= 0 || N0 <= 0 || K <= 0 || N0 % 256 || N1 % 256 || N2 % 256 ||
+        (N1 && !w1) || (N2 && !w2) || !mfma_ok(x, y, N, K)) {
+        snprintf(hd_cuda_errbuf(), 512, "linear_concat3: bad args");
+        return;
+    }
+    GemmArgs g = {};
+    g.A = (const uint16_t *)x;
+    g.B[0] = (const uint16_t *)w0;
+    g.B[1] = (const uint16_t *)(w1 ? w1 : w0);
+    g.B[2] = (const uint16_t *)(w2 ? w2 : w0);
+    g.seg_end[0] = N0;
+    g.seg_end[1] = N0 + N1;
+    g.seg_end[2] = N;
+    g.C = (uint16_t *)y;
+    g.M = M; g.N = N; g.K = K; g.ldc = N;
+    gemm_launch(EPI_NONE, g);
+    hd_check_launch("linear_concat3");
+}

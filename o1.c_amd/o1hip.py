@@ -1,0 +1,307 @@
+"""ctypes bindings of libo1hip.so (the C-ABI declared in include/*.h).
+
+Mirrors the reference's host interface for the per-block forward path:
+hd_linear / hd_sdpa_* / hd_decoder_block / hd_forward / hd_lora_merge_gpu
+(reference: src/cuda/hd_cuda.h, gemm.h, include/hd_cudnn_sdpa.h,
+src/model/block.h, forward.h, include/hd_lora.h). Tensors are torch device
+tensors; only their data pointers cross the boundary.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libo1hip.so")
+
+c_void_p, c_int, c_int64, c_float, c_size_t, c_char_p = (
+    ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t, ctypes.c_char_p)
+
+HD_OK, HD_ERR_MISSING, HD_ERR_OOM, HD_ERR_RUNTIME, HD_ERR_UNSUPPORTED = 0, 6, 7, 8, 9
+HD_ERR_MISMATCH = 5
+
+
+class hd_block_binding(ctypes.Structure):
+    _fields_ = [("layer_idx", c_int)] + [(n, c_void_p) for n in (
+        "q_proj", "k_proj", "v_proj", "o_proj", "input_ln", "post_ln", "gate_proj", "up_proj",
+        "down_proj", "q_norm", "k_norm")]
+
+
+class hd_block_internals(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in ("ln0", "attn_hidden", "attn_resid", "post_ln", "mlp_out")]
+
+
+class hd_block_config(ctypes.Structure):
+    _fields_ = [("eps", c_float), ("rope_theta", c_float), ("attention_scaling", c_float),
+                ("section", c_int64 * 3), ("interleaved", c_int)]
+
+
+class hd_device_alloc(ctypes.Structure):
+    _fields_ = [("dev_ptr", c_void_p), ("nbytes", c_int64), ("name", ctypes.c_char * 256)]
+
+
+class hd_weight_store(ctypes.Structure):
+    _fields_ = [("device_id", c_int), ("allocs", ctypes.POINTER(hd_device_alloc)),
+                ("n_allocs", c_int64), ("arena_ptr", c_void_p), ("arena_bytes", c_int64),
+                ("upload_stream", c_void_p)]
+
+
+class hd_forward_binding(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in (
+        "embed_tokens", "te0_w", "te0_b", "te2_w", "te2_b", "xe1_w", "xe2_w", "xe2_b", "fl_w",
+        "fl_b", "fnorm_w")] + [("n_layers", c_int), ("blocks", ctypes.POINTER(hd_block_binding))]
+
+
+class hd_forward_workspace(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in (
+        "hidden_a", "hidden_b", "h_text", "norm_out", "head_out", "t_emb", "te_hidden", "freq",
+        "freq_bf16", "t_scaled", "xe_stage", "xe_out", "xe_ref")] + [
+        ("n_ref", c_int), ("block_scratch", c_void_p), ("block_scratch_bytes", c_int64),
+        ("sdpa", c_void_p)]
+
+
+class hd_forward_diagnostics(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in (
+        "after_embedding", "after_timestep_conditioning", "after_target_embedding",
+        "after_block_0_input", "after_block_0", "after_block_mid", "after_block_last",
+        "before_final_norm", "after_final_norm", "after_final_head")]
+
+
+class hd_lora_entry(ctypes.Structure):
+    _fields_ = [("lora_prefix", ctypes.c_char * 256), ("base_tensor", ctypes.c_char * 256),
+                ("rank", ctypes.c_uint32), ("in_dim", ctypes.c_uint32),
+                ("out_dim", ctypes.c_uint32), ("alpha", c_float), ("multiplier", c_float),
+                ("down_dev", c_void_p), ("up_dev", c_void_p), ("base_dev", c_void_p)]
+
+
+P = c_void_p
+# name -> (restype, argtypes); every symbol include/*.h declares.
+SIGNATURES = {
+    # hidream_hip.h
+    "hd_last_error": (c_char_p, []),
+    "hd_set_error": (None, [c_char_p]),
+    # hd_hip.h
+    "hd_bf16_to_f32": (c_float, [ctypes.c_uint16]),
+    "hd_f32_to_bf16": (ctypes.c_uint16, [c_float]),
+    "hd_bf16_buf_to_f32": (None, [P, P, c_size_t]),
+    "hd_f32_buf_to_bf16": (None, [P, P, c_size_t]),
+    "hd_cuda_last_error": (c_char_p, []),
+    "hd_cuda_clear_error": (None, []),
+    "hd_hip_set_stream": (None, [P]),
+    "hd_hip_get_stream": (P, []),
+    "hd_hip_sync": (c_int, []),
+    "hd_rmsnorm": (None, [P, P, P, c_int, c_int, c_float]),
+    "hd_silu": (None, [P, P, c_size_t]),
+    "hd_swiglu": (None, [P, P, P, c_size_t]),
+    "hd_residual_add": (None, [P, P, P, c_size_t]),
+    "hd_linear": (None, [P, P, P, P, c_int, c_int, c_int, c_int]),
+    "hd_timestep_embed": (None, [P, P, c_int, c_int]),
+    "hd_mrope_cos_sin": (None, [P, c_int, c_int, P, c_int, c_int, c_float, c_float, c_int, P, P]),
+    "hd_apply_rotary": (None, [P, P, P, P, c_int, c_int, c_int]),
+    "hd_apply_rotary_f32": (None, [P, P, P, P, c_int, c_int, c_int]),
+    "hd_attention_eager": (None, [P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_float]),
+    "hd_head_split": (None, [P, P, c_int, c_int, c_int]),
+    "hd_head_merge": (None, [P, P, c_int, c_int, c_int]),
+    "hd_gather_rows": (None, [P, P, P, c_int, c_int, c_int64]),
+    "hd_apply_tms_condition": (None, [P, P, P, P, c_int, c_int, c_int64]),
+    "hd_scale_f32": (None, [P, P, c_float, c_int]),
+    "hd_f32_convert_bf16": (None, [P, P, c_int]),
+    "hd_sched_bf16_upcast": (None, [P, P, c_int]),
+    "hd_sched_denoised": (None, [P, P, c_float, P, c_int]),
+    "hd_sched_z_next": (None, [P, P, c_float, c_float, P, c_int]),
+    "hd_sched_vcond": (None, [P, P, c_float, P, c_int]),
+    "hd_sched_flow_match_step": (None, [P, P, c_float, c_float, P, c_int]),
+    "hd_sched_cfg_guided": (None, [P, P, c_float, P, c_int]),
+    "hd_add_rmsnorm": (None, [P, P, P, P, P, c_int, c_int, c_float]),
+    "hd_rope_table": (None, [P, c_int, P, c_int, c_int, c_float, c_float, c_int, P]),
+    "hd_qkv_epilogue": (None, [P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float]),
+    "hd_transpose_sd": (None, [P, P, c_int, c_int, c_int]),
+    "hd_patchify_f32": (None, [P, P, c_int, c_int, c_int, c_int]),
+    "hd_unpatchify_f32": (None, [P, P, c_int, c_int, c_int, c_int]),
+    "hd_patchify_bf16": (None, [P, P, c_int, c_int, c_int, c_int]),
+    # hd_gemm.h
+    "hd_gemm_runtime_init": (P, [c_int, c_size_t]),
+    "hd_gemm_runtime_destroy": (None, [P]),
+    "hd_gemm_workspace": (P, [P]),
+    "hd_gemm_workspace_bytes": (c_size_t, [P]),
+    "hd_linear_reference": (None, [P, P, P, P, c_int, c_int, c_int, c_int]),
+    "hd_gemm_set_backend": (None, [c_int]),
+    "hd_gemm_set_prod_backend": (None, [c_int]),
+    "hd_linear_residual": (None, [P, P, P, P, c_int, c_int, c_int]),
+    "hd_linear_swiglu": (None, [P, P, P, P, c_int, c_int, c_int]),
+    "hd_linear_concat3": (None, [P, P, c_int, P, c_int, P, c_int, P, c_int, c_int]),
+    "hd_gemm_config_name": (c_char_p, [c_int, c_int, c_int, c_int]),
+    # hd_sdpa.h
+    "hd_sdpa_create": (c_int, [ctypes.POINTER(c_void_p), c_int, c_int, c_int, c_int, c_int, c_int, c_float]),
+    "hd_sdpa_execute": (c_int, [P, P, P, P, P, P, P]),
+    "hd_sdpa_destroy": (None, [P]),
+    "hd_sdpa_create_split": (c_int, [ctypes.POINTER(c_void_p), c_int, c_int, c_int, c_int, c_int, c_int, c_float]),
+    "hd_sdpa_execute_split": (c_int, [P, P, P, P, P, P]),
+    "hd_sdpa_execute_split_pass": (c_int, [P, c_int, P, P, P, P, P]),
+    "hd_sdpa_create_prod": (c_int, [ctypes.POINTER(c_void_p), c_int, c_int, c_int, c_int, c_int, c_int, c_float]),
+    "hd_flash_attention": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int]),
+    "hd_sdpa_plan_ar_len": (c_int, [P]),
+    "hd_flash_vt_bytes": (c_int64, [c_int, c_int, c_int]),
+    "hd_flash_make_vt": (None, [P, P, c_int, c_int]),
+    # hd_weights.h
+    "hd_weight_store_find": (P, [ctypes.POINTER(hd_weight_store), c_char_p]),
+    # hd_block.h
+    "hd_block_get_config": (None, [ctypes.POINTER(hd_block_config)]),
+    "hd_block_set_config": (None, [ctypes.POINTER(hd_block_config)]),
+    "hd_decoder_block_scratch_bytes": (c_int64, [c_int64, c_int, c_int, c_int, c_int, c_int]),
+    "hd_block_resolve": (c_int, [ctypes.POINTER(hd_weight_store), c_int, ctypes.POINTER(hd_block_binding)]),
+    "hd_decoder_block": (c_int, [P, P, P, ctypes.POINTER(hd_block_binding), P, P, c_int64,
+                                 ctypes.POINTER(hd_block_internals), P, c_int64, c_int, c_int,
+                                 c_int, c_int, c_int, P]),
+    "hd_decoder_block_batched_scratch_bytes": (c_int64, [c_int, c_int64, c_int, c_int, c_int, c_int, c_int]),
+    "hd_decoder_block_batched": (c_int, [P, P, P, c_int, ctypes.POINTER(hd_block_binding), P,
+                                         c_int64, ctypes.POINTER(hd_block_internals), P, c_int,
+                                         c_int64, c_int, c_int, c_int, c_int, c_int]),
+    # hd_forward.h
+    "hd_forward_resolve": (c_int, [ctypes.POINTER(hd_weight_store), c_int, ctypes.POINTER(hd_forward_binding)]),
+    "hd_forward_binding_free": (None, [ctypes.POINTER(hd_forward_binding)]),
+    "hd_forward_workspace_bytes": (c_int64, [c_int64, c_int, c_int, c_int, c_int, c_int, c_int, ctypes.POINTER(c_int64)]),
+    "hd_forward": (c_int, [ctypes.POINTER(hd_forward_binding), ctypes.POINTER(hd_forward_workspace),
+                           P, c_int, P, P, P, c_int, P, P, P, c_int, c_int, c_int, c_int, c_int,
+                           c_int, c_int, ctypes.POINTER(hd_forward_diagnostics), P, P]),
+    "hd_forward_num_layers": (c_int, [ctypes.POINTER(hd_forward_binding)]),
+    "hd_forward_ws_offset": (c_int64, [c_char_p, c_int64, c_int, c_int, c_int, c_int, c_int, c_int, c_int, ctypes.POINTER(c_int64)]),
+    "hd_forward_batched_workspace_bytes": (c_int64, [c_int, c_int64, c_int, c_int, c_int, c_int, c_int, c_int]),
+    "hd_forward_batched": (c_int, [ctypes.POINTER(hd_forward_binding), ctypes.POINTER(hd_forward_workspace),
+                                   c_int, P, c_int, P, c_int, P, c_int, P, c_int, c_int, c_int,
+                                   c_int, c_int, c_int, c_int, ctypes.POINTER(hd_forward_diagnostics), P, P]),
+    # hd_lora.h
+    "hd_lora_merge_gpu": (c_int, [ctypes.POINTER(hd_lora_entry), c_size_t, P]),
+}
+
+_lib = None
+
+
+def load(path=None):
+    """Loads libo1hip.so once and types every exported entry point.
+    Raises RuntimeError when the library (the HIP build) is missing."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = path or LIB_PATH
+    if not os.path.exists(p):
+        raise RuntimeError(
+            f"libo1hip.so not found at {p}: build it first (python -c 'import __graft_entry__ as g; g.build()')")
+    lib = ctypes.CDLL(p)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def bind_torch_stream():
+    """Makes every later launch of the library go to torch's current stream
+    on the current device, so library kernels order with torch's own work."""
+    import torch
+    load().hd_hip_set_stream(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+
+def ptr(t):
+    """Device pointer of a torch tensor (None -> NULL)."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def check_prim(what=""):
+    """Raises if a primitive reported an error through the shared buffer."""
+    msg = load().hd_cuda_last_error()
+    if msg:
+        load().hd_cuda_clear_error()
+        raise RuntimeError(f"{what}: {msg.decode()}")
+
+
+def check_status(st, what=""):
+    if st != HD_OK:
+        raise RuntimeError(f"{what}: status {st}: {load().hd_last_error().decode()}")
+
+
+# ---------------------------------------------------------------------------
+# thin typed helpers (torch tensors in, torch tensors out)
+# ---------------------------------------------------------------------------
+def _torch():
+    import torch
+    return torch
+
+
+def linear(x, w, bias=None, out=None):
+    t = _torch()
+    M, K = x.shape
+    N = w.shape[0]
+    if out is None:
+        out = t.empty((M, N), dtype=t.bfloat16, device=x.device)
+    load().hd_linear(ptr(x), ptr(w), ptr(bias), ptr(out), M, N, K, 1)
+    check_prim("hd_linear")
+    return out
+
+
+def block_config(eps=1e-6, theta=5e6, attention_scaling=1.0, section=(24, 20, 20), interleaved=1):
+    c = hd_block_config()
+    c.eps, c.rope_theta, c.attention_scaling = eps, theta, attention_scaling
+    for i in range(3):
+        c.section[i] = section[i]
+    c.interleaved = interleaved
+    return c
+
+
+def set_block_config(**kw):
+    c = block_config(**kw)
+    load().hd_block_set_config(ctypes.byref(c))
+    return c
+
+
+def binding_from(weights, layer_idx=0):
+    """weights: dict of device tensors with the hd_block_binding field names."""
+    b = hd_block_binding()
+    b.layer_idx = layer_idx
+    for n, _ in hd_block_binding._fields_[1:]:
+        setattr(b, n, weights[n].data_ptr())
+    return b
+
+
+class WeightStore:
+    """hd_weight_store over named torch device tensors (caller keeps them)."""
+
+    def __init__(self, named):
+        self.named = dict(named)
+        arr = (hd_device_alloc * len(self.named))()
+        for i, (n, t) in enumerate(self.named.items()):
+            arr[i].dev_ptr = t.data_ptr()
+            arr[i].nbytes = t.numel() * t.element_size()
+            arr[i].name = n.encode()
+        self._arr = arr
+        self.store = hd_weight_store()
+        self.store.device_id = 0
+        self.store.allocs = ctypes.cast(arr, ctypes.POINTER(hd_device_alloc))
+        self.store.n_allocs = len(self.named)
+
+
+def rope_table(pos, seq, head_dim=128, theta=5e6, section=(24, 20, 20), interleaved=1,
+               attention_scaling=1.0, out=None):
+    t = _torch()
+    if out is None:
+        out = t.empty((seq, head_dim // 2, 2), dtype=t.float32, device=pos.device)
+    sec = (ctypes.c_int64 * 3)(*section)
+    load().hd_rope_table(ptr(pos), seq, sec, 3, head_dim, theta, attention_scaling, interleaved,
+                         ptr(out))
+    check_prim("hd_rope_table")
+    return out
+
+
+class SdpaPlan:
+    def __init__(self, batch, q_heads, kv_heads, seq, head_dim=128, scale=None, ar_len=0):
+        self.h = c_void_p()
+        scale = scale if scale is not None else head_dim ** -0.5
+        rc = load().hd_sdpa_create_prod(ctypes.byref(self.h), batch, q_heads, kv_heads, seq,
+                                        ar_len, head_dim, scale)
+        if rc != 0:
+            raise RuntimeError(load().hd_cuda_last_error().decode())
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.hd_sdpa_destroy(self.h)
+            self.h = None

@@ -1,0 +1,120 @@
+"""GEMM parity: MFMA kernels through the C-ABI vs a torch fp32 reference of
+the same op (x.float() @ w.float().T, one bf16 rounding) and vs the
+reference's known-answer tests (test_gemm_smoke.c:15-20)."""
+import pytest
+import torch
+
+from tests.common import rel_l2, cosine, ulp_diff_bf16, close_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def rnd(shape, g, std=1.0):
+    return (torch.randn(*shape, generator=g) * std).to(torch.bfloat16)
+
+
+SHAPES = [(1152, 6144, 4096), (300, 1024, 512), (1, 4096, 256), (7, 512, 1024), (513, 3072, 1024),
+          (2048, 4096, 12288)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_linear_matches_fp32(pkg, lib, dev, M, N, K):
+    g = torch.Generator().manual_seed(M * 7 + N)
+    x = rnd((M, K), g).to(dev)
+    w = rnd((N, K), g, 0.02).to(dev)
+    y = pkg.linear(x, w)
+    torch.cuda.synchronize()
+    ref = (x.float() @ w.float().t()).to(torch.bfloat16).float()
+    got = y.float()
+    assert rel_l2(got.cpu(), ref.cpu()) < 4e-3
+    assert cosine(got.cpu(), ref.cpu()) > 0.99999
+    # fp32 accumulation in another order: at most a couple of bf16 ulps apart
+    assert close_bf16(got.cpu().numpy(), ref.cpu().numpy(), ulps=2)
+
+
+def test_linear_bias_two_roundings(pkg, lib, dev):
+    g = torch.Generator().manual_seed(3)
+    M, N, K = 130, 1024, 256
+    x, w, b = rnd((M, K), g).to(dev), rnd((N, K), g, 0.05).to(dev), rnd((N,), g).to(dev)
+    y = pkg.linear(x, w, b)
+    torch.cuda.synchronize()
+    acc = (x.float() @ w.float().t()).to(torch.bfloat16).float()
+    ref = (acc + b.float()).to(torch.bfloat16).float()   # gemm.cu:226-235
+    assert close_bf16(y.float().cpu().numpy(), ref.cpu().numpy(), ulps=2)
+    assert rel_l2(y.float().cpu(), ref.cpu()) < 4e-3
+
+
+def test_gemm_smoke_kat(pkg, lib, dev):
+    # test_gemm_smoke.c:15-20: X=[[1,2],[3,4]], W=[[5,6],[7,8]] -> [[17,23],[39,53]]
+    x = torch.tensor([[1., 2.], [3., 4.]], dtype=torch.bfloat16, device=dev)
+    w = torch.tensor([[5., 6.], [7., 8.]], dtype=torch.bfloat16, device=dev)
+    y = pkg.linear(x, w)
+    torch.cuda.synchronize()
+    assert y.float().cpu().tolist() == [[17., 23.], [39., 53.]]
+    # the same KAT through the MFMA path: zero-pad K to 64, N to 256
+    xp = torch.zeros(2, 64, dtype=torch.bfloat16, device=dev)
+    wp = torch.zeros(256, 64, dtype=torch.bfloat16, device=dev)
+    xp[:, :2] = x
+    wp[:2, :2] = w
+    y = pkg.linear(xp, wp)
+    torch.cuda.synchronize()
+    assert y[:, :2].float().cpu().tolist() == [[17., 23.], [39., 53.]]
+    assert float(y[:, 2:].abs().max()) == 0.0
+
+
+def test_linear_residual(pkg, lib, dev):
+    g = torch.Generator().manual_seed(5)
+    M, N, K = 777, 4096, 1024
+    x, w, r = rnd((M, K), g).to(dev), rnd((N, K), g, 0.02).to(dev), rnd((M, N), g).to(dev)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    lib.hd_linear_residual(pkg.ptr(x), pkg.ptr(w), pkg.ptr(r), pkg.ptr(y), M, N, K)
+    pkg.check_prim("linear_residual")
+    torch.cuda.synchronize()
+    o = (x.float() @ w.float().t()).to(torch.bfloat16).float()
+    ref = (r.float() + o).to(torch.bfloat16).float()          # residual.cu:20-22
+    assert rel_l2(y.float().cpu(), ref.cpu()) < 4e-3
+    # o may differ by an ulp of |o| (fp32 accumulation order); the sum is
+    # rounded once more, so the bound is in ulps of |o| + |sum|
+    err = (y.float() - ref).abs()
+    assert bool((err <= 2.0 ** -7 * (o.abs() + ref.abs()) + 1e-6).all())
+
+
+@pytest.mark.parametrize("M", [1152, 70])
+def test_linear_swiglu(pkg, lib, dev, M):
+    g = torch.Generator().manual_seed(6)
+    F, K = 1536, 512
+    x, wg, wu = rnd((M, K), g).to(dev), rnd((F, K), g, 0.05).to(dev), rnd((F, K), g, 0.05).to(dev)
+    y = torch.empty(M, F, dtype=torch.bfloat16, device=dev)
+    lib.hd_linear_swiglu(pkg.ptr(x), pkg.ptr(wg), pkg.ptr(wu), pkg.ptr(y), M, F, K)
+    pkg.check_prim("linear_swiglu")
+    torch.cuda.synchronize()
+    gt = (x.float() @ wg.float().t()).to(torch.bfloat16).float()
+    up = (x.float() @ wu.float().t()).to(torch.bfloat16).float()
+    s = (gt * torch.sigmoid(gt)).to(torch.bfloat16).float()   # act.cu:29-33
+    ref = (s * up).to(torch.bfloat16).float()
+    assert rel_l2(y.float().cpu(), ref.cpu()) < 5e-3
+    assert cosine(y.float().cpu(), ref.cpu()) > 0.99999
+
+
+def test_linear_concat3(pkg, lib, dev):
+    g = torch.Generator().manual_seed(7)
+    M, K = 520, 1024
+    w0, w1, w2 = rnd((1024, K), g, .02).to(dev), rnd((256, K), g, .02).to(dev), rnd((512, K), g, .02).to(dev)
+    x = rnd((M, K), g).to(dev)
+    y = torch.empty(M, 1792, dtype=torch.bfloat16, device=dev)
+    lib.hd_linear_concat3(pkg.ptr(x), pkg.ptr(w0), 1024, pkg.ptr(w1), 256, pkg.ptr(w2), 512,
+                          pkg.ptr(y), M, K)
+    pkg.check_prim("concat3")
+    torch.cuda.synchronize()
+    ref = (x.float() @ torch.cat([w0, w1, w2]).float().t()).to(torch.bfloat16).float()
+    assert close_bf16(y.float().cpu().numpy(), ref.cpu().numpy(), ulps=2)
+
+
+def test_linear_reference_backend(pkg, lib, dev):
+    g = torch.Generator().manual_seed(8)
+    M, N, K = 7, 5, 6     # test_primitives.c:273 shape
+    x, w = rnd((M, K), g).to(dev), rnd((N, K), g).to(dev)
+    y = pkg.linear(x, w)
+    torch.cuda.synchronize()
+    ref = (x.float() @ w.float().t()).to(torch.bfloat16).float()
+    assert close_bf16(y.float().cpu().numpy(), ref.cpu().numpy(), ulps=1)

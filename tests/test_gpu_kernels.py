@@ -1,0 +1,260 @@
+"""Bandwidth kernels and attention through the C-ABI vs the CPU oracle."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from tests.common import rel_l2, cosine, ulp_diff_bf16, close_bf16, grid_pos, bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def dbf(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev, torch.bfloat16)
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("rows,cols", [(37, 4096), (300, 128), (5, 200), (4, 8)])
+def test_rmsnorm(pkg, lib, dev, rows, cols):
+    rng = np.random.default_rng(rows)
+    x = orc.bf16_round(rng.standard_normal((rows, cols)) * 3)
+    w = orc.bf16_round(1 + rng.standard_normal(cols) * 0.1)
+    y = torch.empty(rows, cols, dtype=torch.bfloat16, device=dev)
+    xd, wd = dbf(x, dev), dbf(w, dev)
+    lib.hd_rmsnorm(pkg.ptr(xd), pkg.ptr(wd), pkg.ptr(y), rows, cols, 1e-6)
+    pkg.check_prim("rmsnorm")
+    ref = orc.rmsnorm(x, w, 1e-6, 1)
+    assert close_bf16(host(y), ref, ulps=1, atol_rel=0)
+
+
+def test_add_rmsnorm(pkg, lib, dev):
+    rng = np.random.default_rng(1)
+    x = orc.bf16_round(rng.standard_normal((64, 4096)))
+    a = orc.bf16_round(rng.standard_normal((64, 4096)))
+    w = orc.bf16_round(1 + rng.standard_normal(4096) * 0.1)
+    s = torch.empty(64, 4096, dtype=torch.bfloat16, device=dev)
+    y = torch.empty_like(s)
+    xd, ad, wd = dbf(x, dev), dbf(a, dev), dbf(w, dev)
+    lib.hd_add_rmsnorm(pkg.ptr(xd), pkg.ptr(ad), pkg.ptr(wd), pkg.ptr(s), pkg.ptr(y), 64, 4096, 1e-6)
+    pkg.check_prim("add_rmsnorm")
+    sref = orc.residual_add(x, a, 1)
+    assert np.array_equal(host(s), sref)
+    assert close_bf16(host(y), orc.rmsnorm(sref, w, 1e-6, 1), ulps=1, atol_rel=0)
+
+
+@pytest.mark.parametrize("n", [16, 1000, 4096 * 3 + 5])
+def test_pointwise(pkg, lib, dev, n):
+    rng = np.random.default_rng(n)
+    g = orc.bf16_round(rng.standard_normal(n) * 3)
+    u = orc.bf16_round(rng.standard_normal(n))
+    y = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    gd, ud = dbf(g, dev), dbf(u, dev)
+    lib.hd_swiglu(pkg.ptr(gd), pkg.ptr(ud), pkg.ptr(y), n)
+    pkg.check_prim("swiglu")
+    assert close_bf16(host(y), orc.swiglu(g, u, 1), ulps=1, atol_rel=0)
+    lib.hd_residual_add(pkg.ptr(gd), pkg.ptr(ud), pkg.ptr(y), n)
+    assert np.array_equal(host(y), orc.residual_add(g, u, 1))
+    lib.hd_silu(pkg.ptr(gd), pkg.ptr(y), n)
+    assert close_bf16(host(y), orc.silu(g, 1), ulps=1, atol_rel=0)
+
+
+def test_mrope_and_rotary(pkg, lib, dev):
+    # test_primitives.c:329-388 (seq 4, dim 64, section {6,2,2}, theta 5e6)
+    seq, dim = 4, 64
+    pos = np.zeros((3, seq), np.float32)
+    for i in range(seq):
+        pos[:, i] = [10.0 * (i + 1), 100.0 * (i + 1) + 1, 1000.0 * (i + 1) + 2]
+    sec = (6, 2, 2)
+    c = torch.empty(seq, dim, device=dev)
+    s = torch.empty(seq, dim, device=dev)
+    secd = torch.tensor(sec, dtype=torch.int64, device=dev)
+    posd = torch.from_numpy(pos).to(dev)
+    lib.hd_mrope_cos_sin(pkg.ptr(posd), 1, seq, pkg.ptr(secd), 3, dim, 5e6, 1.0, 1, pkg.ptr(c),
+                         pkg.ptr(s))
+    pkg.check_prim("mrope")
+    cr, sr = orc.mrope_cos_sin(pos, seq, dim, 5e6, sec)
+    assert rel_l2(c.cpu().numpy(), cr) < 2e-5 and rel_l2(s.cpu().numpy(), sr) < 2e-4
+    # rotation with bf16 per-op rounding
+    rng = np.random.default_rng(2)
+    x = orc.bf16_round(rng.standard_normal((3, seq, dim)))
+    y = torch.empty(3, seq, dim, dtype=torch.bfloat16, device=dev)
+    xd, cd, sd = dbf(x, dev), torch.from_numpy(cr).to(dev), torch.from_numpy(sr).to(dev)
+    lib.hd_apply_rotary(pkg.ptr(xd), pkg.ptr(cd), pkg.ptr(sd), pkg.ptr(y), 3, seq, dim)
+    assert np.array_equal(host(y), orc.apply_rotary(x, cr, sr, 1))
+
+
+@pytest.mark.parametrize("B,S", [(1, 200), (2, 256)])
+def test_qkv_epilogue(pkg, lib, dev, B, S):
+    H, KV, D = 4, 2, 128
+    rng = np.random.default_rng(S)
+    qkv = orc.bf16_round(rng.standard_normal((B * S, (H + 2 * KV) * D)) * 2)
+    qn = orc.bf16_round(1 + rng.standard_normal(D) * 0.1)
+    kn = orc.bf16_round(1 + rng.standard_normal(D) * 0.1)
+    pos = grid_pos(S - 10 * 19, 10, 19)
+    posd = torch.from_numpy(pos).to(dev)
+    cs = pkg.rope_table(posd, S, D, theta=1e4)
+    q = torch.empty(B, H, S, D, dtype=torch.bfloat16, device=dev)
+    k = torch.empty(B, KV, S, D, dtype=torch.bfloat16, device=dev)
+    v = torch.empty(B, KV, S, D, dtype=torch.bfloat16, device=dev)
+    qd, qnd, knd = dbf(qkv, dev), dbf(qn, dev), dbf(kn, dev)
+    lib.hd_qkv_epilogue(pkg.ptr(qd), pkg.ptr(qnd), pkg.ptr(knd), pkg.ptr(cs),
+                        pkg.ptr(q), pkg.ptr(k), pkg.ptr(v), None, B, S, H, KV, D, 1e-6)
+    pkg.check_prim("qkv_epilogue")
+    cr, sr = orc.mrope_cos_sin(pos, S, D, 1e4)
+    for b in range(B):
+        rows = qkv[b * S:(b + 1) * S]
+        qh = rows[:, :H * D].reshape(S, H, D).transpose(1, 0, 2)
+        kh = rows[:, H * D:(H + KV) * D].reshape(S, KV, D).transpose(1, 0, 2)
+        vh = rows[:, (H + KV) * D:].reshape(S, KV, D).transpose(1, 0, 2)
+        qr = orc.apply_rotary(orc.rmsnorm(qh, qn, 1e-6, 1), cr, sr, 1)
+        kr = orc.apply_rotary(orc.rmsnorm(kh, kn, 1e-6, 1), cr, sr, 1)
+        # norm sums in another order: rare 1-ulp differences that the
+        # per-op rounded rotation can carry to 2 ulps of the larger term
+        assert close_bf16(host(q[b]), qr, ulps=2, atol_rel=2e-3)
+        assert close_bf16(host(k[b]), kr, ulps=2, atol_rel=2e-3)
+        assert np.mean(host(q[b]) == qr) > 0.98
+        assert np.array_equal(host(v[b]), vh)
+    # V^T layout: same values, transposed, key bits 2/3 exchanged, zero pad
+    spad = (S + 63) // 64 * 64
+    vt = torch.full((B, KV, D, spad), 7.0, dtype=torch.bfloat16, device=dev)
+    lib.hd_qkv_epilogue(pkg.ptr(qd), pkg.ptr(qnd), pkg.ptr(knd), pkg.ptr(cs),
+                        pkg.ptr(q), pkg.ptr(k), None, pkg.ptr(vt), B, S, H, KV, D, 1e-6)
+    pkg.check_prim("qkv_epilogue vt")
+    perm = np.arange(spad)
+    perm = (perm & ~12) | ((perm & 4) << 1) | ((perm & 8) >> 1)
+    vt_h = host(vt)
+    for b in range(B):
+        vh = qkv[b * S:(b + 1) * S, (H + KV) * D:].reshape(S, KV, D).transpose(1, 2, 0)
+        full = np.zeros((KV, D, spad), np.float32)
+        full[:, :, :S] = vh
+        assert np.array_equal(vt_h[b], full[:, :, perm])
+
+
+def _attn_inputs(Hq, Hkv, S, D, seed):
+    rng = np.random.default_rng(seed)
+    q = orc.bf16_round(rng.standard_normal((Hq, S, D)))
+    k = orc.bf16_round(rng.standard_normal((Hkv, S, D)))
+    v = orc.bf16_round(rng.standard_normal((Hkv, S, D)))
+    return q, k, v
+
+
+@pytest.mark.parametrize("Hq,Hkv,S,ar", [(8, 2, 256, 0), (4, 4, 200, 0), (4, 1, 333, 50),
+                                         (32, 8, 1152, 0)])
+def test_flash_vs_oracle(pkg, lib, dev, Hq, Hkv, S, ar):
+    D = 128
+    q, k, v = _attn_inputs(Hq, Hkv, S, D, S + Hq)
+    plan = pkg.SdpaPlan(1, Hq, Hkv, S, D, ar_len=ar)
+    out = torch.empty(Hq, S, D, dtype=torch.bfloat16, device=dev)
+    qd, kd, vd = dbf(q, dev), dbf(k, dev), dbf(v, dev)
+    rc = lib.hd_sdpa_execute(plan.h, pkg.ptr(qd), pkg.ptr(kd), pkg.ptr(vd), None, pkg.ptr(out), None)
+    assert rc == 0, lib.hd_cuda_last_error()
+    ref = orc.attention(q, k, v, None, ar, round_=0)            # [S, Hq*D] fp32
+    got = host(out).transpose(1, 0, 2).reshape(S, Hq * D)
+    assert rel_l2(got, ref) < 8e-3 and cosine(got, ref) > 0.99995
+
+
+def test_flash_dense_mask_and_invariants(pkg, lib, dev):
+    Hq, Hkv, S, D = 2, 1, 96, 128
+    q, k, v = _attn_inputs(Hq, Hkv, S, D, 11)
+    rng = np.random.default_rng(3)
+    mask = np.where(rng.random((S, S)) < 0.3, -3.3895e38, 0.0).astype(np.float32)
+    np.fill_diagonal(mask, 0.0)
+    mb = dbf(mask, dev)
+    plan = pkg.SdpaPlan(1, Hq, Hkv, S, D)
+    out = torch.empty(Hq, S, D, dtype=torch.bfloat16, device=dev)
+    qd, kd, vd = dbf(q, dev), dbf(k, dev), dbf(v, dev)
+    rc = lib.hd_sdpa_execute(plan.h, pkg.ptr(qd), pkg.ptr(kd), pkg.ptr(vd), pkg.ptr(mb), pkg.ptr(out),
+                             None)
+    assert rc == 0
+    ref = orc.attention(q, k, v, host(mb), 0, round_=0)
+    got = host(out).transpose(1, 0, 2).reshape(S, Hq * D)
+    assert rel_l2(got, ref) < 8e-3
+    # invariant: q = 0 -> uniform probabilities -> every row is mean(V)
+    z = torch.zeros(Hq, S, D, dtype=torch.bfloat16, device=dev)
+    rc = lib.hd_sdpa_execute(plan.h, pkg.ptr(z), pkg.ptr(kd), pkg.ptr(vd), None, pkg.ptr(out), None)
+    assert rc == 0
+    mean_v = v[0].mean(axis=0)
+    assert np.abs(host(out)[0] - mean_v[None, :]).max() < 2e-2
+
+
+def test_eager_matches_oracle(pkg, lib, dev):
+    # test_primitives.c:441-535 shape class, fp32 softmax, bf16 probs
+    Hq, Hkv, S, D = 2, 1, 3, 4
+    q = orc.bf16_round(np.array([(i % 13) * 0.11 for i in range(Hq * S * D)]).reshape(Hq, S, D))
+    k = orc.bf16_round(np.array([(i % 7) * 0.13 for i in range(Hkv * S * D)]).reshape(Hkv, S, D))
+    v = orc.bf16_round(np.array([(i % 5) * 0.17 for i in range(Hkv * S * D)]).reshape(Hkv, S, D))
+    mask = orc.bf16_round(np.array([0.0 if i % 3 == 0 else -3.3895e38 for i in range(S * S)]).reshape(S, S))
+    sc = torch.empty(Hq, S, S, dtype=torch.bfloat16, device=dev)
+    pr = torch.empty_like(sc)
+    out = torch.empty(S, Hq, D, dtype=torch.bfloat16, device=dev)
+    qd, kd, vd, md = dbf(q, dev), dbf(k, dev), dbf(v, dev), dbf(mask, dev)
+    lib.hd_attention_eager(pkg.ptr(qd), pkg.ptr(kd), pkg.ptr(vd), pkg.ptr(md), pkg.ptr(sc),
+                           pkg.ptr(pr), pkg.ptr(out), Hq, Hkv, S, D, D ** -0.5)
+    pkg.check_prim("eager")
+    ref = orc.attention(q, k, v, host(md), 0, prob_mode=1, round_=1)
+    assert close_bf16(host(out).reshape(S, Hq * D), ref, ulps=1, atol_rel=0)
+
+
+def test_head_split_merge_roundtrip(pkg, lib, dev):
+    # test_primitives.c:537-556, bit-exact
+    S, H, D = 37, 4, 128
+    x = torch.randn(S, H, D, device=dev).to(torch.bfloat16)
+    y = torch.empty_like(x)
+    z = torch.empty_like(x)
+    lib.hd_head_split(pkg.ptr(x), pkg.ptr(y), S, H, D)
+    lib.hd_head_merge(pkg.ptr(y), pkg.ptr(z), S, H, D)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(H, S, D), x.transpose(0, 1).contiguous())
+    assert torch.equal(z, x)
+
+
+def test_lora_merge(pkg, lib, dev):
+    N, K, R = 300, 520, 64
+    rng = np.random.default_rng(9)
+    w = orc.bf16_round(rng.standard_normal((N, K)) * 0.02)
+    up = (rng.standard_normal((N, R)) * 0.01).astype(np.float32)
+    down = (rng.standard_normal((R, K)) * 0.01).astype(np.float32)
+    wd = dbf(w, dev)
+    upd, dnd = torch.from_numpy(up).to(dev), torch.from_numpy(down).to(dev)
+    e = pkg.hd_lora_entry()
+    e.rank, e.in_dim, e.out_dim, e.alpha, e.multiplier = R, K, N, 32.0, 0.8
+    e.down_dev, e.up_dev, e.base_dev = dnd.data_ptr(), upd.data_ptr(), wd.data_ptr()
+    st = lib.hd_lora_merge_gpu(ctypes.byref(e), 1, None)
+    assert st == 0
+    torch.cuda.synchronize()
+    ref = orc.lora_merge(w, up, down, 0.8 * 32.0 / R)
+    assert close_bf16(host(wd), ref, ulps=1, atol_rel=0)
+    assert np.mean(host(wd) == ref) > 0.99
+
+
+def test_sched_and_patchify_bit_exact(pkg, lib, dev):
+    rng = np.random.default_rng(4)
+    n = 3 * 64 * 64
+    z = orc.bf16_round(rng.standard_normal(n))
+    xp = orc.bf16_round(rng.standard_normal(n))
+    mo = torch.empty(n, device=dev)
+    zd, xpd = dbf(z, dev), dbf(xp, dev)
+    lib.hd_sched_vcond(pkg.ptr(zd), pkg.ptr(xpd), 0.7, pkg.ptr(mo), n)
+    assert np.array_equal(mo.cpu().numpy(), orc.sched_vcond(z, xp, 0.7))
+    zn = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    lib.hd_sched_flow_match_step(pkg.ptr(zd), pkg.ptr(mo), 0.7, 0.6, pkg.ptr(zn), n)
+    assert np.array_equal(host(zn), orc.sched_flow_match_step(z, mo.cpu().numpy(), 0.7, 0.6))
+    c = rng.standard_normal(n).astype(np.float32)
+    u = rng.standard_normal(n).astype(np.float32)
+    o = torch.empty(n, device=dev)
+    cd, ud = torch.from_numpy(c).to(dev), torch.from_numpy(u).to(dev)
+    lib.hd_sched_cfg_guided(pkg.ptr(cd), pkg.ptr(ud), 5.0, pkg.ptr(o), n)
+    assert np.array_equal(o.cpu().numpy(), orc.sched_cfg_guided(c, u, 5.0))
+    img = rng.standard_normal((3, 64, 96)).astype(np.float32)
+    tok = torch.empty(2 * 3, 3 * 32 * 32, device=dev)
+    imgd = torch.from_numpy(img).to(dev)
+    lib.hd_patchify_f32(pkg.ptr(imgd), pkg.ptr(tok), 3, 2, 3, 32)
+    assert np.array_equal(tok.cpu().numpy(), orc.patchify(img, 32))
+    back = torch.empty_like(imgd)
+    lib.hd_unpatchify_f32(pkg.ptr(tok), pkg.ptr(back), 3, 2, 3, 32)
+    assert torch.equal(back, imgd)
