@@ -69,6 +69,13 @@ void hd_linear_concat3(const void *x_dev, const void *w0, int N0,
                        const void *w1, int N1, const void *w2, int N2,
                        void *y_dev, int M, int K);
 
+/* Diagnostics/tuning: launches tuning-table configuration `cfg` (0..8)
+ * with epilogue 0 (plain, N outputs) or 3 (SwiGLU: w0 = gate, w1 = up, N =
+ * F outputs). Returns 0 when launched, non-zero for an unknown config or
+ * unsupported shape. */
+int hd_gemm_tune_run(int cfg, int epi, const void *x, const void *w0, const void *w1, void *y,
+                     int M, int N, int K);
+
 /* Name of the kernel configuration hd_linear* would launch for a shape
  * (diagnostics; static string). */
 const char *hd_gemm_config_name(int M, int N, int K, int epilogue);

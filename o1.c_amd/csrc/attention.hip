@@ -31,6 +31,7 @@
 #define FA_D 128
 #define FA_BQ 128      // queries per block (4 waves x 32)
 #define FA_BK 64       // keys per tile
+#define FA_TAU 8.0f    // lazy-rescale threshold (log2 units)
 
 __host__ __device__ __forceinline__ int perm16(int s) {
     return (s & ~12) | ((s & 4) << 1) | ((s & 8) >> 1);
@@ -47,10 +48,22 @@ struct FaArgs {
     int ar_len;            // rows < ar_len: causal
     int q_row_end;         // only rows < q_row_end are computed/written
     float scale_log2;      // scale * log2(e)
+    float inv_scale;       // 1 / scale (mask values are added to raw scores)
     int out_seq_major;
 };
 
 __device__ __forceinline__ void fa_wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// max / sum with the lane 32 positions away (v_permlane32_swap exchanges
+// the two 32-lane halves; max/sum of the pair is the same in both lanes)
+__device__ __forceinline__ float xor32_max(float v) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 template <bool MASKED>
 __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
@@ -145,54 +158,53 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
             }
         }
 
-        // scale, mask, tile max
+        // tile max on raw scores (the positive scale commutes with max)
         const int kv0 = t * FA_BK;
         float mt = -INFINITY;
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                float v = s[j][r] * a.scale_log2;
+                float v = s[j][r];
                 if (MASKED) {
                     const int kv = kv0 + j * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
                     bool dead = kv >= a.S || (my_q < a.ar_len && kv > my_q);
                     if (a.mask && !dead && my_q < a.S)
-                        v += bf2f(a.mask[(size_t)my_q * a.S + kv]) * 1.44269504088896341f;
+                        v += bf2f(a.mask[(size_t)my_q * a.S + kv]) * a.inv_scale;
                     if (dead) v = -INFINITY;
+                    s[j][r] = v;
                 }
-                s[j][r] = v;
                 mt = fmaxf(mt, v);
             }
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-        const float m_new = fmaxf(m_run, mt);
-        const float alpha = exp2f(m_run - m_new);
-        m_run = m_new;
-        float psum = 0.f;
-        bf16x8_t pf[4];
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int hh = 0; hh < 2; hh++) {
-                uint32_t w[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    float p0 = exp2f(s[j][hh * 8 + 2 * e] - m_new);
-                    float p1 = exp2f(s[j][hh * 8 + 2 * e + 1] - m_new);
-                    // row sum over the bf16-rounded probabilities the MFMA sees
-                    uint32_t pk = pack_bf2(p0, p1);
-                    psum += lo_bf(pk) + hi_bf(pk);
-                    w[e] = pk;
-                }
-                u32x4_t wv = {w[0], w[1], w[2], w[3]};
-                pf[j * 2 + hh] = __builtin_bit_cast(bf16x8_t, wv);
-            }
-        l_run = l_run * alpha + psum;
-        if (__builtin_amdgcn_read_exec() && alpha != 1.0f) {
+        mt = xor32_max(mt);
+        // Lazy rescale: the running max only moves when some row's tile max
+        // exceeds it by more than 2^FA_TAU in probability terms, so the O
+        // rescale is rare after the first tiles; p stays <= 2^FA_TAU.
+        if (__builtin_amdgcn_ballot_w64((mt - m_run) * a.scale_log2 > FA_TAU)) {
+            const float m_new = fmaxf(m_run, mt);
+            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * a.scale_log2);
+            m_run = m_new;
+            l_run *= alpha;
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) o[i][r] *= alpha;
         }
+        const float mc = -m_run * a.scale_log2;
+        bf16x8_t pf[4];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                bf16x8_t pv;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    float p = __builtin_amdgcn_exp2f(fmaf(s[j][hh * 8 + e], a.scale_log2, mc));
+                    l_run += p;
+                    pv[e] = (__bf16)p;
+                }
+                pf[j * 2 + hh] = pv;
+            }
         // O^T += V^T . P^T over 4 steps of 16 keys
 #pragma unroll
         for (int st = 0; st < 4; st++) {
@@ -209,7 +221,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
     }
 
     // ---- normalise and store ----------------------------------------------
-    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float l_tot = xor32_sum(l_run);
     const float inv = 1.0f / l_tot;
     if (my_q >= a.q_row_end) return;
     uint16_t *dst;
@@ -279,6 +291,7 @@ static int fa_launch(const void *q, const void *k, const void *vt, const void *m
     a.ar_len = ar_len;
     a.q_row_end = q_row_end;
     a.scale_log2 = scale * 1.44269504088896341f;
+    a.inv_scale = 1.0f / scale;
     a.out_seq_major = out_seq_major;
     const int nqt = (q_row_end + FA_BQ - 1) / FA_BQ;
     dim3 grid((unsigned)((size_t)batch * hq * nqt));

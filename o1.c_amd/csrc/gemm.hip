@@ -64,11 +64,11 @@ __device__ __forceinline__ int xcd_remap(int b, int nb) {
     return xcd * per + (xcd < rem ? xcd : rem) + idx;
 }
 
-template <int BM, int BN, int WGM, int WGN, int EPI>
+template <int BM, int BN, int WGM, int WGN, int EPI, int PF = 0, int GROUP_M = 8, int SWZ = 0,
+          int DIAG = 0>
 __global__ __launch_bounds__(WGM * WGN * 64) void gemm_bf16_kernel(GemmArgs g) {
     using Cfg = GemmCfg<BM, BN, WGM, WGN, EPI>;
     constexpr int NW = Cfg::NW, WTM = Cfg::WTM, WTN = Cfg::WTN, TM = Cfg::TM, TN = Cfg::TN;
-    constexpr int GROUP_M = 8;
     __shared__ __attribute__((aligned(1024))) uint16_t smem[Cfg::LDS_BYTES / 2];
 
     const int lane = threadIdx.x & 63;
@@ -89,17 +89,20 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_bf16_kernel(GemmArgs g) {
     constexpr int AI = BM / 8 / NW, BI = BN / 8 / NW;
     const uint16_t *a_src[AI];
     const uint16_t *b_src[BI];
+    // LDS slot (row, s) holds 16-byte chunk s ^ swz(row) of the row, so the
+    // fragment reads of 16 consecutive rows spread over all banks.
+    auto swz = [](int r) { return SWZ ? ((r >> 1) & 7) : (r & 7); };
     const int sub = lane >> 3;                  // row within an 8-row group
-    const int chunk = (lane & 7) ^ sub;         // swizzled 16-byte chunk
 #pragma unroll
     for (int i = 0; i < AI; i++) {
         int r = (wave * AI + i) * 8 + sub;
         int m = min(m0 + r, g.M - 1);
-        a_src[i] = g.A + (size_t)m * g.K + chunk * 8;
+        a_src[i] = g.A + (size_t)m * g.K + ((lane & 7) ^ swz(r)) * 8;
     }
 #pragma unroll
     for (int i = 0; i < BI; i++) {
         int r = (wave * BI + i) * 8 + sub;
+        const int chunk = (lane & 7) ^ swz(r);
         const uint16_t *p;
         if (EPI == EPI_SWIGLU) {
             int grp = r / WTN, j = r % WTN;
@@ -137,14 +140,42 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_bf16_kernel(GemmArgs g) {
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
     const int nk = g.K / 64;
-    const int l32 = lane & 31, khalf = lane >> 5, sw = lane & 7;
+    const int l32 = lane & 31, khalf = lane >> 5;
+    const int sw = SWZ ? ((l32 >> 1) & 7) : (lane & 7);   // swz(row): row = 32*t + l32
     issue(0, 0);
     wait_vm0();
     __syncthreads();
     for (int kt = 0; kt < nk; kt++) {
         const int buf = kt & 1;
-        if (kt + 1 < nk) issue(kt + 1, buf ^ 1);
+        if (kt + 1 < nk && DIAG != 1) issue(kt + 1, buf ^ 1);   // DIAG 1: compute only
         const uint16_t *As = As0 + buf * BM * 64, *Bs = Bs0 + buf * BN * 64;
+        if (DIAG == 2) {
+            // load-only diagnostic: one fragment read, no MFMA
+            acc[0][0][0] += (float)(*(const bf16x8_t *)(As + l32 * 64))[0];
+        } else if (PF) {
+            // fragments of k-step ks+1 are read while the MFMAs of ks run
+            bf16x8_t af[2][TM], bw[2][TN];
+            auto ld = [&](int ks, int slot) {
+                const int c = ((ks * 2 + khalf) ^ sw) * 8;
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+                    af[slot][i] = *(const bf16x8_t *)(As + (wm * WTM + i * 32 + l32) * 64 + c);
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    bw[slot][j] = *(const bf16x8_t *)(Bs + (wn * WTN + j * 32 + l32) * 64 + c);
+            };
+            ld(0, 0);
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                if (ks < 3) ld(ks + 1, (ks + 1) & 1);
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[ks & 1][j], af[ks & 1][i],
+                                                                             acc[i][j], 0, 0, 0);
+            }
+        } else {
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             const int c = ((ks * 2 + khalf) ^ sw) * 8;
@@ -160,6 +191,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_bf16_kernel(GemmArgs g) {
 #pragma unroll
                 for (int j = 0; j < TN; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[j], af[i], acc[i][j], 0, 0, 0);
+        }
         }
         wait_vm0();
         __syncthreads();
@@ -201,6 +233,231 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_bf16_kernel(GemmArgs g) {
 #pragma unroll 4
     for (int r0 = 0; r0 < WTM; r0 += RPI) {
         const int r = r0 + lane / CPR, cc = (lane % CPR) * 8;
+        const int m = gm0 + r, n = gn0 + cc;
+        if (m < g.M && n < g.N) {
+            u32x4_t v = *(const u32x4_t *)(stg + r * LDW + cc);
+            if (EPI == EPI_BIAS || EPI == EPI_RES) {
+                u32x4_t o = EPI == EPI_BIAS ? *(const u32x4_t *)(g.bias + n)
+                                            : *(const u32x4_t *)(g.res + (size_t)m * g.ldc + n);
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    v[e] = pack_bf2(lo_bf(v[e]) + lo_bf(o[e]), hi_bf(v[e]) + hi_bf(o[e]));
+            }
+            *(u32x4_t *)(g.C + (size_t)m * g.ldc + n) = v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Multi-stage variant: an NS-deep LDS ring of BK-wide K tiles. Tile kt+NS-1
+// is requested while tile kt is consumed, and the wait before each barrier
+// only drains the oldest outstanding tile (s_waitcnt vmcnt(N)), so NS-1
+// tiles of global->LDS traffic stay in flight behind the MFMAs.
+// ---------------------------------------------------------------------------
+template <int N> __device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Waits until at most N of this wave's global->LDS loads are outstanding,
+// then joins the workgroup barrier. Written as one asm statement: the
+// compiler's __syncthreads() lowering adds a full vmcnt(0) drain, which
+// would empty the prefetch ring at every K step. The memory clobber keeps
+// LDS reads from moving across the barrier.
+template <int N> __device__ __forceinline__ void wait_vm_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI>
+struct MsCfg {
+    static constexpr int NW = WGM * WGN, NT = NW * 64;
+    static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
+    static constexpr int WTN_OUT = EPI == EPI_SWIGLU ? WTN / 2 : WTN;
+    static constexpr int BN_OUT = EPI == EPI_SWIGLU ? BN / 2 : BN;
+    static constexpr int CPR = BK / 8;            // 16-byte chunks per tile row
+    static constexpr int RPI = 64 / CPR;          // rows per wave load instruction
+    static constexpr int AI = BM / RPI / NW, BI = BN / RPI / NW;   // load instrs per wave
+    static constexpr int LPT = AI + BI;           // per tile per wave
+    static constexpr int STAGE = (BM + BN) * BK;  // elements per stage
+    static constexpr int EPAD = 8;
+    static constexpr int MAIN_BYTES = NS * STAGE * 2;
+    static constexpr int EPI_BYTES = NW * WTM * (WTN_OUT + EPAD) * 2;
+    static constexpr int LDS_BYTES = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
+    static_assert(BK == 32 || BK == 64, "BK");
+    static_assert(BM % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "loader split");
+    static_assert((NS - 2) * LPT < 64, "vmcnt");
+};
+
+// chunk swizzle: 16 consecutive rows of a tile map to 16 distinct 16-byte
+// bank groups (64 banks x 4 bytes)
+template <int CPR> __device__ __forceinline__ int ms_swz(int r) {
+    return CPR == 8 ? ((r >> 1) & 7) : ((r >> 2) & 3);
+}
+
+template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 0>
+__global__ __launch_bounds__(WGM * WGN * 64) void gemm_ms_kernel(GemmArgs g) {
+    using C = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI>;
+    constexpr int WTM = C::WTM, WTN = C::WTN, TM = C::TM, TN = C::TN, CPR = C::CPR;
+    constexpr int AI = C::AI, BI = C::BI, GROUP_M = 8;
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[C::LDS_BYTES / 2];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int nblk = g.ntm * g.ntn;
+    const int lin = xcd_remap(blockIdx.x, nblk);
+    const int in_group = GROUP_M * g.ntn;
+    const int first_m = (lin / in_group) * GROUP_M;
+    const int gm = min(g.ntm - first_m, GROUP_M);
+    const int tm = first_m + (lin % in_group) % gm;
+    const int tn = (lin % in_group) / gm;
+    const int m0 = tm * BM;
+
+    const uint16_t *a_src[AI];
+    const uint16_t *b_src[BI];
+    const int sub = lane / CPR, cl = lane % CPR;
+#pragma unroll
+    for (int i = 0; i < AI; i++) {
+        int r = (wave * AI + i) * C::RPI + sub;
+        int m = min(m0 + r, g.M - 1);
+        a_src[i] = g.A + (size_t)m * g.K + (cl ^ ms_swz<CPR>(r)) * 8;
+    }
+#pragma unroll
+    for (int i = 0; i < BI; i++) {
+        int r = (wave * BI + i) * C::RPI + sub;
+        const uint16_t *p;
+        if (EPI == EPI_SWIGLU) {
+            int grp = r / WTN, j = r % WTN;
+            int n = tn * C::BN_OUT + grp * (WTN / 2) + (j % (WTN / 2));
+            n = min(n, g.N - 1);
+            p = (j < WTN / 2 ? g.B[0] : g.B[1]) + (size_t)n * g.K;
+        } else {
+            int n = min(tn * BN + r, g.seg_end[2] - 1);
+            int sg = n < g.seg_end[0] ? 0 : (n < g.seg_end[1] ? 1 : 2);
+            int base = sg == 0 ? 0 : g.seg_end[sg - 1];
+            p = g.B[sg] + (size_t)(n - base) * g.K;
+        }
+        b_src[i] = p + (cl ^ ms_swz<CPR>(r)) * 8;
+    }
+    auto issue = [&](int kt, int st) {
+        uint16_t *As = smem + st * C::STAGE, *Bs = As + BM * BK;
+#pragma unroll
+        for (int i = 0; i < AI; i++)
+            __builtin_amdgcn_global_load_lds((const void *)(a_src[i] + kt * BK),
+                                             (HD_LDS void *)(As + (wave * AI + i) * 512), 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < BI; i++)
+            __builtin_amdgcn_global_load_lds((const void *)(b_src[i] + kt * BK),
+                                             (HD_LDS void *)(Bs + (wave * BI + i) * 512), 16, 0, 0);
+    };
+
+    f32x16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    const int nk = g.K / BK;
+    const int l32 = lane & 31, khalf = lane >> 5;
+    const int sw = ms_swz<CPR>(l32);
+#pragma unroll
+    for (int s = 0; s < NS - 1; s++)
+        if (s < nk) issue(s, s);
+    for (int kt = 0; kt < nk; kt++) {
+        if (kt + NS - 2 < nk) wait_vm_barrier<(NS - 2) * C::LPT>();
+        else wait_vm_barrier<0>();
+        if (kt + NS - 1 < nk) issue(kt + NS - 1, (kt + NS - 1) % NS);
+        const uint16_t *As = smem + (kt % NS) * C::STAGE, *Bs = As + BM * BK;
+        if (SGB) {
+            // register double buffer of fragments; the reads of k-step ks+1
+            // are interleaved one by one with the MFMAs of ks
+            bf16x8_t af[2][TM], bw[2][TN];
+            auto ld = [&](int ks, int sl) {
+                const int c = ((ks * 2 + khalf) ^ sw) * 8;
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+                    af[sl][i] = *(const bf16x8_t *)(As + (wm * WTM + i * 32 + l32) * BK + c);
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    bw[sl][j] = *(const bf16x8_t *)(Bs + (wn * WTN + j * 32 + l32) * BK + c);
+            };
+            ld(0, 0);
+#pragma unroll
+            for (int ks = 0; ks < BK / 16; ks++) {
+                if (ks + 1 < BK / 16) ld(ks + 1, (ks + 1) & 1);
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[ks & 1][j], af[ks & 1][i],
+                                                                             acc[i][j], 0, 0, 0);
+                if (ks + 1 < BK / 16) {
+                    constexpr int NR = TM + TN, NM = TM * TN;
+#pragma unroll
+                    for (int q = 0; q < NR; q++) {
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);        // 1 DS read
+                        __builtin_amdgcn_sched_group_barrier(0x008, NM / NR, 0);  // MFMAs
+                    }
+                    __builtin_amdgcn_sched_group_barrier(0x008, NM - (NM / NR) * NR, 0);
+                }
+            }
+        } else {
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ks++) {
+            const int c = ((ks * 2 + khalf) ^ sw) * 8;
+            bf16x8_t af[TM], bw[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                af[i] = *(const bf16x8_t *)(As + (wm * WTM + i * 32 + l32) * BK + c);
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                bw[j] = *(const bf16x8_t *)(Bs + (wn * WTN + j * 32 + l32) * BK + c);
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[j], af[i], acc[i][j], 0, 0, 0);
+        }
+        }
+    }
+    __syncthreads();   // every wave is done with the ring before staging reuses it
+
+    constexpr int WO = C::WTN_OUT, LDW = WO + C::EPAD;
+    uint16_t *stg = smem + wave * WTM * LDW;
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        const int row = i * 32 + l32;
+#pragma unroll
+        for (int j = 0; j < (EPI == EPI_SWIGLU ? TN / 2 : TN); j++) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float x = acc[i][j][q * 4 + e];
+                    if (EPI == EPI_SWIGLU) {
+                        float gt = bfround(x);
+                        float up = bfround(acc[i][j + TN / 2][q * 4 + e]);
+                        float sg = bfround(gt * (1.0f / (1.0f + __expf(-gt))));
+                        x = sg * up;
+                    }
+                    v[e] = x;
+                }
+                const int col = j * 32 + q * 8 + khalf * 4;
+                u32x2_t pk = {pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+                *(u32x2_t *)(stg + row * LDW + col) = pk;
+            }
+        }
+    }
+    __syncthreads();
+    constexpr int CPRO = WO / 8, RPIO = 64 / CPRO;
+    const int gm0 = m0 + wm * WTM;
+    const int gn0 = tn * C::BN_OUT + wn * WO;
+#pragma unroll 4
+    for (int r0 = 0; r0 < WTM; r0 += RPIO) {
+        const int r = r0 + lane / CPRO, cc = (lane % CPRO) * 8;
         const int m = gm0 + r, n = gn0 + cc;
         if (m < g.M && n < g.N) {
             u32x4_t v = *(const u32x4_t *)(stg + r * LDW + cc);
@@ -280,26 +537,67 @@ extern "C" size_t hd_gemm_workspace_bytes(hd_gemm_runtime *rt) { return rt ? rt-
 extern "C" void hd_gemm_set_backend(int p) { g_use_production = p; }
 extern "C" void hd_gemm_set_prod_backend(int b) { g_prod_backend = b; }
 
-template <int BM, int BN, int WGM, int WGN, int EPI>
+template <int BM, int BN, int WGM, int WGN, int EPI, int PF = 0, int GM = 8, int SWZ = 0, int DIAG = 0>
 static void launch_cfg(GemmArgs &g) {
     using Cfg = GemmCfg<BM, BN, WGM, WGN, EPI>;
     g.ntm = (g.M + BM - 1) / BM;
     g.ntn = (g.N + Cfg::BN_OUT - 1) / Cfg::BN_OUT;
-    gemm_bf16_kernel<BM, BN, WGM, WGN, EPI><<<g.ntm * g.ntn, Cfg::NT, 0, hd_stream()>>>(g);
+    gemm_bf16_kernel<BM, BN, WGM, WGN, EPI, PF, GM, SWZ, DIAG>
+        <<<g.ntm * g.ntn, Cfg::NT, 0, hd_stream()>>>(g);
 }
 
-// Tile configuration per shape. "big" (256x256, 4 waves of 128x128) when the
-// grid holds enough tiles to fill 256 CUs, else 128x128 tiles.
+template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 0>
+static void launch_ms(GemmArgs &g) {
+    using Cfg = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI>;
+    g.ntm = (g.M + BM - 1) / BM;
+    g.ntn = (g.N + Cfg::BN_OUT - 1) / Cfg::BN_OUT;
+    gemm_ms_kernel<BM, BN, BK, NS, WGM, WGN, EPI, SGB><<<g.ntm * g.ntn, Cfg::NT, 0, hd_stream()>>>(g);
+}
+
+// Tuning table: every configuration that hd_gemm_tune_run can launch.
+template <int EPI>
+static bool run_table(int cfg, GemmArgs &g) {
+    switch (cfg) {
+    case 0: launch_cfg<256, 256, 2, 2, EPI, 0, 8, 1>(g); return true;       // 4 waves, 2 stages
+    case 1: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1>(g); return true;       // 8 waves
+    case 2: launch_cfg<128, 128, 2, 2, EPI>(g); return true;
+    case 3: launch_ms<256, 256, 64, 2, 2, 4, EPI, 1>(g); return true;      // production, main
+    case 4: launch_ms<192, 256, 64, 2, 2, 4, EPI, 1>(g); return true;      // production, 192 rows
+    case 5: launch_ms<192, 256, 64, 2, 2, 4, EPI>(g); return true;
+    case 6: launch_ms<256, 256, 32, 4, 2, 4, EPI, 1>(g); return true;      // 4-stage ring
+    case 7: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 1>(g); return true;    // diag: compute only
+    case 8: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 2>(g); return true;    // diag: loads only
+    default: return false;
+    }
+}
+
+// Tile configuration per shape. The 8-wave 256-wide kernels are the main
+// path; a 192-row tile is taken when it quantises the grid onto the 256 CUs
+// better (M = 8704: 34 -> 46 row tiles), and 128x128 tiles for grids too
+// small to fill the chip twice with 256x256 tiles.
+static double quant_eff(long tiles) {
+    long rounds = (tiles + 255) / 256;
+    return (double)tiles / (double)(rounds * 256);
+}
+
 template <int EPI>
 static const char *pick_and_launch(GemmArgs &g, bool launch) {
-    const int bn_out_big = EPI == EPI_SWIGLU ? 128 : 256;
-    long tiles_big = (long)((g.M + 255) / 256) * ((g.N + bn_out_big - 1) / bn_out_big);
-    if (tiles_big >= 256) {
-        if (launch) launch_cfg<256, 256, 2, 2, EPI>(g);
-        return "bf16_256x256x64_w2x2";
+    const int bn_out = EPI == EPI_SWIGLU ? 128 : 256;
+    const long tn = (g.N + bn_out - 1) / bn_out;
+    const long t256 = (long)((g.M + 255) / 256) * tn;
+    const long t192 = (long)((g.M + 191) / 192) * tn;
+    if (t256 < 512) {
+        if (launch) launch_cfg<128, 128, 2, 2, EPI>(g);
+        return "bf16_128x128x64_w2x2";
     }
-    if (launch) launch_cfg<128, 128, 2, 2, EPI>(g);
-    return "bf16_128x128x64_w2x2";
+    // 192-row tiles compute 25% fewer rows per tile for the same overheads;
+    // take them only when the quantisation gain outweighs that (~12%).
+    if (quant_eff(t192) > quant_eff(t256) * 1.12) {
+        if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 1>(g);
+        return "bf16_192x256x64_w2x4_ilv";
+    }
+    if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 1>(g);
+    return "bf16_256x256x64_w2x4_ilv";
 }
 
 static bool mfma_ok(const void *x, const void *y, int N, int K) {
@@ -313,6 +611,23 @@ static void gemm_launch(int epi, GemmArgs &g) {
     case EPI_RES: pick_and_launch<EPI_RES>(g, true); break;
     case EPI_SWIGLU: pick_and_launch<EPI_SWIGLU>(g, true); break;
     }
+}
+
+// Diagnostics: runs tuning-table configuration `cfg` (0..8) for
+// epilogue 0 (plain) or 3 (SwiGLU, w1 = up). Returns 0 when launched.
+extern "C" int hd_gemm_tune_run(int cfg, int epi, const void *x, const void *w0, const void *w1,
+                                void *y, int M, int N, int K) {
+    if (!x || !w0 || !y || M <= 0 || N <= 0 || K <= 0 || !mfma_ok(x, y, N, K)) return 1;
+    GemmArgs g = {};
+    g.A = (const uint16_t *)x;
+    g.B[0] = g.B[2] = (const uint16_t *)w0;
+    g.B[1] = (const uint16_t *)(w1 ? w1 : w0);
+    g.seg_end[0] = g.seg_end[1] = g.seg_end[2] = N;
+    g.C = (uint16_t *)y;
+    g.M = M; g.N = N; g.K = K; g.ldc = N;
+    bool ok = epi == EPI_SWIGLU ? (w1 && run_table<EPI_SWIGLU>(cfg, g)) : run_table<EPI_NONE>(cfg, g);
+    if (!ok) return 1;
+    return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
 extern "C" const char *hd_gemm_config_name(int M, int N, int K, int epi) {

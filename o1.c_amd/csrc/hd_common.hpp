@@ -12,22 +12,21 @@ hipStream_t hd_stream(void);
 void hd_check_launch(const char *what);
 
 // ---- bf16 <-> fp32 ------------------------------------------------------
-// bf16 payloads are uint16_t; conversion is IEEE round-to-nearest-even on
-// the bit pattern (the reference's rule, support.cu:21-28). Finite inputs
-// only matter on this path; NaN payloads are not produced by it.
+// bf16 payloads are uint16_t. fp32 -> bf16 uses gfx950's v_cvt_pk_bf16_f32,
+// IEEE round-to-nearest-even: for finite values the same bits as the
+// reference's integer rule (support.cu:21-28); NaN payloads are not produced
+// on this path.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float bf2f(uint16_t b) {
     return __uint_as_float(((uint32_t)b) << 16);
 }
-__device__ __forceinline__ uint16_t f2bf(float f) {
-    uint32_t u = __float_as_uint(f);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
-}
-__device__ __forceinline__ float bfround(float f) { return bf2f(f2bf(f)); }
-// Two floats -> packed bf16x2 (low half = a).
+// Two floats -> packed bf16x2 (low half = a), one instruction.
 __device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
-    return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+    bf16x2_t v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
 }
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+__device__ __forceinline__ float bfround(float f) { return bf2f(f2bf(f)); }
 __device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
