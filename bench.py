@@ -1,6 +1,6 @@
 """Benchmark of the o1 denoiser step on MI355X (one GPU).
 
-Workload: one full denoising-step forward at
+Workload (benchmark configuration 1): one full denoising-step forward at
 1024x1024 - 36 decoder blocks (hidden 4096, 32x128 heads, 8 kv heads, FFN
 12288), 4096 image tokens (64x64 grid) + 256 text tokens = 4352 per
 sequence, batch 2 (CFG cond/uncond), t-embedder MLP at t=0.5, x_embedder,
@@ -46,6 +46,9 @@ def main():
     ap.add_argument("--layers", type=int, default=L)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=20)
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="run only the dominant kernel (gate/up GEMM + SwiGLU at the step's "
+                         "shape) and a 1 GiB device copy, for rocprofv3 counter passes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on exactly one GPU (the reference has no multi-GPU "
@@ -67,10 +70,13 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.init()
     pkg.bind_torch_stream()
+    if args.kernel_only:
+        kernel_only(pkg, lib, B * S, args.kernel_iters)
+        return
     print(f"[bench] building {args.layers}-layer synthetic model", file=sys.stderr, flush=True)
     tensors = synth.build_model(n_layers=args.layers, seed=0, device="cuda:0")
     model = synth.Model(tensors, args.layers)
-    pkg.set_block_config(theta=1e4)          # 2D RoPE, theta 1e4
+    pkg.set_block_config(theta=1e4)          # 2D RoPE, theta 1e4 (synthetic benchmark configurations)
 
     # synthetic inputs: text ids (last = timestep token), latents N(0,1) seed 42
     g = torch.Generator().manual_seed(42)
@@ -183,7 +189,7 @@ def main():
         "wall_s": round(wall, 3),
         "roofline": {"kernel": "gemm_bf16 gate/up + SwiGLU epilogue", "bound": "mfma",
                      "achieved": round(achieved, 1), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved * 1e12 / PEAK_BF16, 4), "traffic": None,
+                     "frac": round(achieved * 1e12 / PEAK_BF16, 4), "traffic": read_traffic(),
                      "launch_ms": round(kms, 4), "shape": [M, 2 * FF, HID]},
         "attention": {"kernel": "flash_fwd (full, GQA 32/8, D=128)", "achieved": round(attn_tf, 1),
                       "unit": "TFLOP/s", "frac": round(attn_tf * 1e12 / PEAK_BF16, 4),
@@ -191,6 +197,39 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(res))
+
+
+def kernel_only(pkg, lib, M, iters):
+    """Dominant kernel alone + a copy of known size (the counter calibration)."""
+    import ctypes
+    import torch
+    dev = torch.device("cuda:0")
+    x = torch.randn(M, HID, device=dev).to(torch.bfloat16)
+    wg = (torch.randn(FF, HID, device=dev) * 0.02).to(torch.bfloat16)
+    wu = (torch.randn(FF, HID, device=dev) * 0.02).to(torch.bfloat16)
+    y = torch.empty(M, FF, dtype=torch.bfloat16, device=dev)
+    src = torch.ones(1 << 29, dtype=torch.int16, device=dev)     # 1 GiB
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(iters):
+        lib.hd_linear_swiglu(pkg.ptr(x), pkg.ptr(wg), pkg.ptr(wu), pkg.ptr(y), M, FF, HID)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"kernel_only": True, "M": M, "iters": iters, "copy_bytes": 1 << 30}))
+
+
+def read_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed counter
+    summary (two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled by
+    a 1 GiB copy's counters); None when absent."""
+    path = os.path.join(ROOT, "profiles", "gemm_swiglu_c1_traffic.txt")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(S, T, gh, gw, B, layers):

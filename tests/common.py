@@ -39,7 +39,7 @@ def to_dev(t, dev):
 def grid_pos(text_len, gh, gw, row_offset=0, fix_point=0):
     """pos [3, S] fp32 for `text_len` text tokens at position 0 followed by a
     gh x gw image grid: (T, H, W) = (fix_point, row + row_offset, col). The
-    BASELINE 2D-RoPE layout (text at 0, image rows/cols)."""
+    2D-RoPE layout of the benchmark configurations (text at 0, image rows/cols)."""
     S = text_len + gh * gw
     pos = np.zeros((3, S), np.float32)
     r, c = np.divmod(np.arange(gh * gw), gw)

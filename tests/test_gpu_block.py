@@ -126,7 +126,7 @@ def test_block_split_plan_causal_prefix(pkg, lib, dev):
 
 
 def test_block_config0_full_size(pkg, lib, dev):
-    """1024 image tokens (32x32) + 128 text, hidden 4096,
+    """Benchmark configuration 0: 1024 image tokens (32x32) + 128 text, hidden 4096,
     32x128 heads (8 kv), FFN 12288, 2D RoPE theta 1e4, text at position 0."""
     H, KV, HID, FF, D = 32, 8, 4096, 12288, 128
     T, gh, gw = 128, 32, 32
