@@ -294,8 +294,8 @@ template <int CPR> __device__ __forceinline__ int ms_swz(int r) {
     return CPR == 8 ? ((r >> 1) & 7) : ((r >> 2) & 3);
 }
 
-template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 0>
-__global__ __launch_bounds__(WGM * WGN * 64) void gemm_ms_kernel(GemmArgs g) {
+template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 0, int OCC = 1>
+__global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g) {
     using C = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI>;
     constexpr int WTM = C::WTM, WTN = C::WTN, TM = C::TM, TN = C::TN, CPR = C::CPR;
     constexpr int AI = C::AI, BI = C::BI, GROUP_M = 8;
@@ -372,7 +372,9 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_ms_kernel(GemmArgs g) {
         const uint16_t *As = smem + (kt % NS) * C::STAGE, *Bs = As + BM * BK;
         if (SGB) {
             // register double buffer of fragments; the reads of k-step ks+1
-            // are interleaved one by one with the MFMAs of ks
+            // are interleaved one by one with the MFMAs of ks (SGB 2: the
+            // tile's global->LDS loads, issued above, are spread between
+            // the MFMAs as well instead of leaving as one burst)
             bf16x8_t af[2][TM], bw[2][TN];
             auto ld = [&](int ks, int sl) {
                 const int c = ((ks * 2 + khalf) ^ sw) * 8;
@@ -384,23 +386,24 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_ms_kernel(GemmArgs g) {
                     bw[sl][j] = *(const bf16x8_t *)(Bs + (wn * WTN + j * 32 + l32) * BK + c);
             };
             ld(0, 0);
+            constexpr int KS = BK / 16, NR = TM + TN, NM = TM * TN;
+            constexpr int NV = SGB == 2 ? (C::LPT + KS - 1) / KS : 0;   // VMEM per k-step
 #pragma unroll
-            for (int ks = 0; ks < BK / 16; ks++) {
-                if (ks + 1 < BK / 16) ld(ks + 1, (ks + 1) & 1);
+            for (int ks = 0; ks < KS; ks++) {
+                if (ks + 1 < KS) ld(ks + 1, (ks + 1) & 1);
 #pragma unroll
                 for (int i = 0; i < TM; i++)
 #pragma unroll
                     for (int j = 0; j < TN; j++)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[ks & 1][j], af[ks & 1][i],
                                                                              acc[i][j], 0, 0, 0);
-                if (ks + 1 < BK / 16) {
-                    constexpr int NR = TM + TN, NM = TM * TN;
+                const int nr = ks + 1 < KS ? NR : 0;
+                const int nv = NV;
 #pragma unroll
-                    for (int q = 0; q < NR; q++) {
-                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);        // 1 DS read
-                        __builtin_amdgcn_sched_group_barrier(0x008, NM / NR, 0);  // MFMAs
-                    }
-                    __builtin_amdgcn_sched_group_barrier(0x008, NM - (NM / NR) * NR, 0);
+                for (int q = 0; q < NM; q++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);        // 1 MFMA
+                    if (q < nr) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // 1 DS read
+                    else if (q - nr < nv) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 VMEM
                 }
             }
         } else {
@@ -546,12 +549,12 @@ static void launch_cfg(GemmArgs &g) {
         <<<g.ntm * g.ntn, Cfg::NT, 0, hd_stream()>>>(g);
 }
 
-template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 0>
+template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 0, int OCC = 1>
 static void launch_ms(GemmArgs &g) {
     using Cfg = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI>;
     g.ntm = (g.M + BM - 1) / BM;
     g.ntn = (g.N + Cfg::BN_OUT - 1) / Cfg::BN_OUT;
-    gemm_ms_kernel<BM, BN, BK, NS, WGM, WGN, EPI, SGB><<<g.ntm * g.ntn, Cfg::NT, 0, hd_stream()>>>(g);
+    gemm_ms_kernel<BM, BN, BK, NS, WGM, WGN, EPI, SGB, OCC><<<g.ntm * g.ntn, Cfg::NT, 0, hd_stream()>>>(g);
 }
 
 // Tuning table: every configuration that hd_gemm_tune_run can launch.
@@ -565,6 +568,16 @@ static bool run_table(int cfg, GemmArgs &g) {
     case 4: launch_ms<192, 256, 64, 2, 2, 4, EPI, 1>(g); return true;      // production, 192 rows
     case 5: launch_ms<192, 256, 64, 2, 2, 4, EPI>(g); return true;
     case 6: launch_ms<256, 256, 32, 4, 2, 4, EPI, 1>(g); return true;      // 4-stage ring
+    case 9: launch_ms<256, 256, 64, 2, 2, 4, EPI, 2>(g); return true;      // loads spread
+    case 10: launch_ms<256, 256, 32, 4, 2, 2, EPI, 2>(g); return true;
+    case 11: launch_ms<256, 256, 32, 4, 2, 4, EPI, 2>(g); return true;
+    case 12: launch_ms<192, 256, 64, 2, 2, 4, EPI, 2>(g); return true;
+    case 13: launch_ms<256, 256, 64, 2, 2, 2, EPI, 2>(g); return true;
+    case 14: launch_ms<256, 128, 32, 3, 2, 2, EPI, 1, 2>(g); return true;   // 2 blocks / CU
+    case 15: launch_ms<128, 256, 32, 3, 2, 2, EPI, 1, 2>(g); return true;
+    case 16: launch_ms<256, 128, 32, 3, 2, 2, EPI, 2, 2>(g); return true;
+    case 17: launch_ms<192, 128, 32, 3, 2, 2, EPI, 1, 2>(g); return true;
+    case 18: launch_ms<128, 128, 64, 2, 2, 2, EPI, 1, 2>(g); return true;
     case 7: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 1>(g); return true;    // diag: compute only
     case 8: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 2>(g); return true;    // diag: loads only
     default: return false;
@@ -587,8 +600,8 @@ static const char *pick_and_launch(GemmArgs &g, bool launch) {
     const long t256 = (long)((g.M + 255) / 256) * tn;
     const long t192 = (long)((g.M + 191) / 192) * tn;
     if (t256 < 512) {
-        if (launch) launch_cfg<128, 128, 2, 2, EPI>(g);
-        return "bf16_128x128x64_w2x2";
+        if (launch) launch_ms<128, 128, 64, 2, 2, 2, EPI, 1, 2>(g);
+        return "bf16_128x128x64_w2x2_occ2";
     }
     // 192-row tiles compute 25% fewer rows per tile for the same overheads;
     // take them only when the quantisation gain outweighs that (~12%).

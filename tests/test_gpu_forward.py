@@ -1,0 +1,156 @@
+"""Whole-denoiser parity: hd_forward / hd_forward_batched (t-embedder, token
+embedding + timestep-token substitution, x_embedder, blocks, final norm and
+head; forward.c:190-404) on the GPU vs the CPU oracle's forward."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from tests.common import make_block_weights, rel_l2, cosine, grid_pos, bf16
+
+pytestmark = pytest.mark.gpu
+
+VOCAB, TMS = 151936, 151673
+
+
+def make_forward_weights(n_layers, HID, H, KV, FF, D, seed):
+    g = torch.Generator().manual_seed(seed)
+
+    def r(*shape, std=0.02):
+        return bf16(torch.randn(*shape, generator=g) * std)
+    fw = {
+        "embed_tokens": r(VOCAB, HID, std=1.0),
+        "te0_w": r(HID, 256), "te0_b": r(HID), "te2_w": r(HID, HID), "te2_b": r(HID),
+        "xe1_w": r(1024, 3072), "xe2_w": r(HID, 1024, std=0.05), "xe2_b": r(HID),
+        "fl_w": r(3072, HID), "fl_b": r(3072), "fnorm_w": bf16(1 + torch.randn(HID, generator=g) * 0.02),
+        "blocks": [make_block_weights(HID, H, KV, FF, D, seed=seed + 1 + i) for i in range(n_layers)],
+    }
+    return fw
+
+
+def store_names(fw):
+    L = "model.language_model."
+    names = {L + "embed_tokens.weight": fw["embed_tokens"],
+             "model.t_embedder1.mlp.0.weight": fw["te0_w"], "model.t_embedder1.mlp.0.bias": fw["te0_b"],
+             "model.t_embedder1.mlp.2.weight": fw["te2_w"], "model.t_embedder1.mlp.2.bias": fw["te2_b"],
+             "model.x_embedder.proj1.weight": fw["xe1_w"], "model.x_embedder.proj2.weight": fw["xe2_w"],
+             "model.x_embedder.proj2.bias": fw["xe2_b"], "model.final_layer2.linear.weight": fw["fl_w"],
+             "model.final_layer2.linear.bias": fw["fl_b"], L + "norm.weight": fw["fnorm_w"]}
+    slot = {"q_proj": "self_attn.q_proj.weight", "k_proj": "self_attn.k_proj.weight",
+            "v_proj": "self_attn.v_proj.weight", "o_proj": "self_attn.o_proj.weight",
+            "input_ln": "input_layernorm.weight", "post_ln": "post_attention_layernorm.weight",
+            "gate_proj": "mlp.gate_proj.weight", "up_proj": "mlp.up_proj.weight",
+            "down_proj": "mlp.down_proj.weight", "q_norm": "self_attn.q_norm.weight",
+            "k_norm": "self_attn.k_norm.weight"}
+    for i, b in enumerate(fw["blocks"]):
+        for k, v in b.items():
+            names[f"{L}layers.{i}.{slot[k]}"] = v
+    return names
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_forward_vs_oracle(pkg, lib, dev, split):
+    nL, HID, H, KV, FF, D = 2, 512, 4, 2, 1024, 128
+    T, gh, gw = 24, 8, 10
+    I = gh * gw
+    S = T + I
+    theta = 5e6 if split else 1e4
+    fw = make_forward_weights(nL, HID, H, KV, FF, D, seed=11)
+    rng = np.random.default_rng(3)
+    ids = rng.integers(0, 151643, T).astype(np.int64)
+    ids[-1] = TMS
+    ids[3] = -5          # out of range -> padding row 0 (embed.cu:24)
+    vin = bf16(torch.from_numpy(rng.standard_normal((I, 3072)).astype(np.float32))).numpy()
+    pos = grid_pos(T, gh, gw)
+    ar = 0
+    if split:
+        pos[:, :T] = np.arange(T)[None]
+        pos[:, T:] += 4096
+        ar = T - 1
+    t = 0.37
+    # GPU
+    pkg.set_block_config(theta=theta)
+    tens = {k: v.to(dev, torch.bfloat16) for k, v in store_names(fw).items()}
+    ws_store = pkg.WeightStore(tens)
+    fb = pkg.hd_forward_binding()
+    pkg.check_status(lib.hd_forward_resolve(ctypes.byref(ws_store.store), nL, ctypes.byref(fb)), "resolve")
+    assert lib.hd_forward_num_layers(ctypes.byref(fb)) == nL
+    nbytes = lib.hd_forward_workspace_bytes(S, I, H, KV, HID, FF, D, None)
+    wsbuf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    ws = pkg.hd_forward_workspace()
+    ws.hidden_a = wsbuf.data_ptr()
+    plan = pkg.SdpaPlan(1, H, KV, S, D, ar_len=ar) if split else None
+    if plan:
+        ws.sdpa = plan.h.value
+    idsd = torch.from_numpy(ids).to(dev)
+    posd = torch.from_numpy(pos).to(dev)
+    vind = torch.from_numpy(vin).to(dev, torch.bfloat16)
+    td = torch.tensor([t], dtype=torch.float32, device=dev)
+    out = torch.empty(S, 3072, dtype=torch.bfloat16, device=dev)
+    diag = pkg.hd_forward_diagnostics()
+    blk0 = torch.empty(S, HID, dtype=torch.bfloat16, device=dev)
+    diag.after_block_0 = blk0.data_ptr()
+    st = lib.hd_forward(ctypes.byref(fb), ctypes.byref(ws), pkg.ptr(idsd), T, pkg.ptr(posd), None,
+                        pkg.ptr(vind), I, None, pkg.ptr(td), None, S, H, KV, HID, FF, D, TMS,
+                        ctypes.byref(diag), pkg.ptr(out), None)
+    pkg.check_status(st, "hd_forward")
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    lib.hd_forward_binding_free(ctypes.byref(fb))
+    # oracle
+    ofw = {k: (v.numpy() if not isinstance(v, list) else [{kk: vv.numpy() for kk, vv in b.items()}
+                                                           for b in v]) for k, v in fw.items()}
+    for faithful, bound in ((1, 5e-3), (0, 1e-2)):
+        cfg = orc.block_cfg(H, KV, HID, FF, D, theta=theta, faithful=faithful, ar_len=ar)
+        ref, blocks = orc.forward(ofw, cfg, ids, vin, t, pos, TMS, keep_blocks=True)
+        r, c = rel_l2(got, ref), cosine(got, ref)
+        rb = rel_l2(blk0.float().cpu().numpy(), blocks[0])
+        print(f"forward split={split} faithful={faithful}: rel_l2={r:.3e} cos={c:.7f} block0={rb:.3e}")
+        assert r <= bound and c >= 0.9999 and rb <= bound
+
+
+def test_forward_batched_matches_single(pkg, lib, dev):
+    import importlib
+    synth = importlib.import_module("o1c_amd.synthetic")
+    nL, HID, H, KV, FF, D = 2, 512, 4, 2, 1024, 128
+    T, I = 16, 64
+    S = T + I
+    B = 2
+    tens = synth.build_model(n_layers=nL, hidden=HID, heads=H, kv_heads=KV, ff=FF, seed=5)
+    model = synth.Model(tens, nL)
+    pkg.set_block_config(theta=1e4)
+    pos = grid_pos(T, 8, 8)
+    posd = torch.from_numpy(pos).to(dev)
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, 151643, (B, T), generator=g)
+    ids[:, -1] = TMS
+    idsd = ids.to(dev)
+    vin = torch.randn(B, I, 3072, generator=g).to(dev, torch.bfloat16)
+    td = torch.tensor([0.5, 0.8], device=dev)
+    wsb = lib.hd_forward_batched_workspace_bytes(B, S, I, H, KV, HID, FF, D)
+    buf = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    ws = pkg.hd_forward_workspace()
+    ws.hidden_a = buf.data_ptr()
+    out = torch.empty(B, S, 3072, dtype=torch.bfloat16, device=dev)
+    st = lib.hd_forward_batched(ctypes.byref(model.binding), ctypes.byref(ws), B, pkg.ptr(idsd), T,
+                                pkg.ptr(posd), 0, pkg.ptr(vin), I, pkg.ptr(td), S, H, KV, HID, FF, D,
+                                TMS, None, pkg.ptr(out), None)
+    pkg.check_status(st, "batched")
+    for b in range(B):
+        w1 = torch.empty(lib.hd_forward_workspace_bytes(S, I, H, KV, HID, FF, D, None),
+                         dtype=torch.uint8, device=dev)
+        ws1 = pkg.hd_forward_workspace()
+        ws1.hidden_a = w1.data_ptr()
+        o1 = torch.empty(S, 3072, dtype=torch.bfloat16, device=dev)
+        idb = idsd[b].contiguous()
+        vb = vin[b].contiguous()
+        tb = td[b:b + 1].contiguous()
+        st = lib.hd_forward(ctypes.byref(model.binding), ctypes.byref(ws1), pkg.ptr(idb), T,
+                            pkg.ptr(posd), None, pkg.ptr(vb), I, None, pkg.ptr(tb), None, S, H, KV,
+                            HID, FF, D, TMS, None, pkg.ptr(o1), None)
+        pkg.check_status(st, "single")
+        torch.cuda.synchronize()
+        # same kernels, M differs (B*S vs S rows): GEMM tiles differ -> a few ulps
+        assert rel_l2(out[b].float().cpu(), o1.float().cpu()) < 5e-3
