@@ -10,6 +10,7 @@ A "step" = one hd_forward_batched call over both CFG sequences.
 Prints ONE JSON line (driver contract) with roofline and cpu_baseline.
 """
 import argparse
+import ctypes
 import json
 import os
 import platform
@@ -23,8 +24,15 @@ PEAK_BF16 = 2.5e15      # dense bf16 MFMA, MI355X
 PEAK_HBM = 8.0e12
 
 CFGS = {
-    "c1": dict(name="denoise_step_1024sq_cfg2", batch=2, text=256, gh=64, gw=64),
-    "c2": dict(name="denoise_step_2048sq", batch=1, text=256, gh=128, gw=128),
+    "c1": dict(name="denoise_step_1024sq_cfg2", batch=2, text=256, gh=64, gw=64, refs=0),
+    "c2": dict(name="denoise_step_2048sq", batch=1, text=256, gh=128, gw=128, refs=0),
+    # multi-reference edit: 64x64 target + 3 references of 64x64 (+64 RoPE
+    # rows each, x_embedder rows cached) + 512 text tokens = 16896
+    "c3": dict(name="edit_step_3refs_1024sq", batch=1, text=512, gh=64, gw=64, refs=3),
+    # LoRA merge (r=64, all q/k/v/o/gate/up/down of 36 blocks) + 28-step
+    # flow-match Euler sampler, CFG batch 2, guidance 5, shift 3
+    "c4": dict(name="lora_merge_plus_28step_euler_cfg_1024sq", batch=2, text=256, gh=64, gw=64,
+               refs=0, steps=28, guidance=5.0, shift=3.0, rank=64),
 }
 HID, NH, NKV, FF, D, L = 4096, 32, 8, 12288, 128, 36
 
@@ -64,8 +72,8 @@ def main():
     synth = import_module("o1c_amd.synthetic")
 
     cfg = CFGS[args.config]
-    B, T, gh, gw = cfg["batch"], cfg["text"], cfg["gh"], cfg["gw"]
-    I = gh * gw
+    B, T, gh, gw, R = cfg["batch"], cfg["text"], cfg["gh"], cfg["gw"], cfg["refs"]
+    I = gh * gw * (1 + R)
     S = T + I
     dev = torch.device("cuda:0")
     torch.cuda.init()
@@ -87,16 +95,33 @@ def main():
     ids[:, -1] = synth.TMS_ID
     ids = ids.to(dev)
     tsd = torch.full((B,), 0.5, dtype=torch.float32, device=dev)
+    # 2D RoPE positions: text at 0; target grid, then each reference grid
+    # with a +64 row offset per reference
     pos = np.zeros((3, S), np.float32)
-    r, c = np.divmod(np.arange(I), gw)
-    pos[1, T:], pos[2, T:] = r, c
+    segs = 1 + R
+    gha = (ctypes.c_int * segs)(*([gh] * segs))
+    gwa = (ctypes.c_int * segs)(*([gw] * segs))
+    roa = (ctypes.c_int * segs)(*[64 * k for k in range(segs)])
+    assert lib.hd_seq_grid_positions(T, segs, gha, gwa, roa, None, 0.0, pkg.np_ptr(pos)) == S
     posd = torch.from_numpy(pos).to(dev)
     wsb = lib.hd_forward_batched_workspace_bytes(B, S, I, NH, NKV, HID, FF, D)
     wsbuf = torch.empty(wsb, dtype=torch.uint8, device=dev)
     ws = pkg.hd_forward_workspace()
     ws.hidden_a = wsbuf.data_ptr()
     out = torch.empty(B, S, 3072, dtype=torch.bfloat16, device=dev)
-    import ctypes
+    extra = {}
+    if R:
+        # reference rows are clean fixed N(0,1) content: their x_embedder rows
+        # are computed once and reused every step (forward.c:301-313)
+        n_ref = gh * gw * R
+        ref_rows = vin[0, I - n_ref:].contiguous()
+        xs = pkg.linear(ref_rows, tensors["model.x_embedder.proj1.weight"])
+        xe_ref = pkg.linear(xs, tensors["model.x_embedder.proj2.weight"],
+                            tensors["model.x_embedder.proj2.bias"])
+        ws.xe_ref = xe_ref.data_ptr()
+        ws.n_ref = n_ref
+    if args.config == "c4":
+        extra = run_c4(pkg, lib, model, tensors, cfg, ws, ids, posd, vin, T, I, S, dev, args)
 
     def step():
         st = lib.hd_forward_batched(ctypes.byref(model.binding), ctypes.byref(ws), B, pkg.ptr(ids), T,
@@ -167,9 +192,12 @@ def main():
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(S, T, gh, gw, B, args.layers)
 
+    metric = {"c1": "DiT denoise steps/sec (1024^2, CFG batch 2, 36 blocks)",
+              "c2": "DiT denoise steps/sec (2048^2, 36 blocks)",
+              "c3": "DiT edit steps/sec (1024^2 target + 3 references, 36 blocks)",
+              "c4": "DiT denoise steps/sec (1024^2, CFG batch 2) + LoRA merge and 28-step image"}
     res = {
-        "metric": "DiT denoise steps/sec (1024^2, CFG batch 2, 36 blocks)" if args.config == "c1"
-                  else "DiT denoise steps/sec (2048^2, 36 blocks)",
+        "metric": metric[args.config],
         "value": round(steps_per_s, 4),
         "unit": "steps/s",
         "n_gpus": 1,
@@ -189,14 +217,89 @@ def main():
         "wall_s": round(wall, 3),
         "roofline": {"kernel": "gemm_bf16 gate/up + SwiGLU epilogue", "bound": "mfma",
                      "achieved": round(achieved, 1), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved * 1e12 / PEAK_BF16, 4), "traffic": read_traffic(),
+                     "frac": round(achieved * 1e12 / PEAK_BF16, 4),
+                     "traffic": read_traffic() if args.config in ("c1", "c4") else None,
                      "launch_ms": round(kms, 4), "shape": [M, 2 * FF, HID]},
         "attention": {"kernel": "flash_fwd (full, GQA 32/8, D=128)", "achieved": round(attn_tf, 1),
                       "unit": "TFLOP/s", "frac": round(attn_tf * 1e12 / PEAK_BF16, 4),
                       "launch_ms": round(ams, 4)},
         "cpu_baseline": cpu,
     }
+    res.update(extra)
     print(json.dumps(res))
+
+
+def run_c4(pkg, lib, model, tensors, cfg, ws, ids, posd, vin, T, I, S, dev, args):
+    """LoRA merge of every q/k/v/o/gate/up/down weight of the 36 blocks on the
+    GPU (rank 64, A,B ~ N(0, 0.01), scale 1.0), then one image: 28-step
+    flow-match Euler with CFG (guidance 5, sigmas linear 1 -> 0 with shift 3)
+    from the seeded initial latent, all through the C-ABI."""
+    import numpy as np
+    import torch
+    r = cfg["rank"]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    names = ["self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+             "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj"]
+    entries = (pkg.hd_lora_entry * (len(names) * L))()
+    keep = []
+    k = 0
+    for layer in range(L):
+        for nm in names:
+            w = tensors[f"model.language_model.layers.{layer}.{nm}.weight"]
+            N, K = w.shape
+            up = torch.empty(N, r, device=dev).normal_(0, 0.01, generator=gen)
+            down = torch.empty(r, K, device=dev).normal_(0, 0.01, generator=gen)
+            keep += [up, down]
+            e = entries[k]
+            e.rank, e.in_dim, e.out_dim, e.alpha, e.multiplier = r, K, N, float(r), 1.0
+            e.up_dev, e.down_dev, e.base_dev = up.data_ptr(), down.data_ptr(), w.data_ptr()
+            k += 1
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    st = lib.hd_lora_merge_gpu(entries, k, None)
+    e1.record()
+    torch.cuda.synchronize()
+    if st != 0:
+        raise RuntimeError(lib.hd_last_error().decode())
+    merge_ms = e0.elapsed_time(e1)
+    welems = sum(int(tensors[f"model.language_model.layers.0.{nm}.weight"].numel()) for nm in names) * L
+    # sampler
+    steps, g, shift = cfg["steps"], cfg["guidance"], cfg["shift"]
+    sch = pkg.hd_scheduler()
+    n = lib.hd_scheduler_derive_default(ctypes.byref(sch), steps, shift, 8.0)
+    sig = (ctypes.c_float * n)(*sch.sigmas[:n])
+    side = cfg["gh"] * 32      # 3072-d patch features = 3 x 32 x 32 pixels
+    noise = np.empty(3 * side * side, np.float32)
+    lib.hd_initial_noise(42, side, side, pkg.np_ptr(noise))
+    noised = torch.from_numpy(noise).to(dev)
+    z = torch.empty(I, 3072, dtype=torch.bfloat16, device=dev)
+    lib.hd_patchify_bf16(pkg.ptr(noised), pkg.ptr(z), 3, cfg["gh"], cfg["gw"], 32)
+    sb = lib.hd_denoise_scratch_bytes(S, I, steps)
+    scratch = torch.empty(sb, dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    st = lib.hd_denoise_euler_cfg(ctypes.byref(model.binding), ctypes.byref(ws), pkg.ptr(ids), T,
+                                  pkg.ptr(posd), 0, pkg.ptr(z), I, sig, steps, g, S, NH, NKV, HID,
+                                  FF, D, 151673, pkg.ptr(scratch), sb, None)
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    if st != 0:
+        raise RuntimeError(lib.hd_last_error().decode())
+    img_s = e0.elapsed_time(e1) / 1000.0
+    zf = z.float()
+    assert torch.isfinite(zf).all(), "non-finite latent"
+    return {"lora": {"targets": k, "rank": r, "merge_ms": round(merge_ms, 3),
+                     "weight_elems": welems,
+                     "hbm_gb_s": round(welems * 4 / (merge_ms * 1e-3) / 1e9, 1),
+                     "fp32_tflops": round(welems * 2 * r / (merge_ms * 1e-3) / 1e12, 2)},
+            "sampler": {"steps": steps, "guidance": g, "shift": shift,
+                        "sigmas_first_last": [round(sch.sigmas[0], 6), round(sch.sigmas[steps - 1], 6)],
+                        "s_per_image": round(img_s, 3), "wall_s": round(wall, 3),
+                        "latent_std": round(float(zf.std()), 4)}}
 
 
 def kernel_only(pkg, lib, M, iters):

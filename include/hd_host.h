@@ -1,0 +1,118 @@
+#ifndef HD_HOST_H
+#define HD_HOST_H
+
+/*
+ * Host-side modules around the forward: the seeded initial noise (torch CPU
+ * MT19937 randn), the sampler sigma schedules, position-id / mask tables and
+ * the flow-match Euler + CFG denoising loop that drives hd_forward_batched.
+ *
+ * Replaces (same names, same struct layouts, same results):
+ *   src/runtime/torch_rng.h:30-56     hd_torch_rng_*  / hd_torch_randn_f32
+ *   src/model/scheduler.h             hd_scheduler_* (sigma derivations, Euler step)
+ *   src/runtime/sequence.c:102-142    T2I position ids and causal-prefix mask
+ *   src/runtime/generate.c:78-104     initial noise (seed + 1) and pixel_unshuffle
+ */
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "hidream_hip.h"
+#include "hd_forward.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- torch CPU MT19937 (torch_rng.h:30-56) ---------------------------- */
+typedef struct hd_torch_rng {
+    uint64_t seed_;
+    int left_;
+    int seeded_;
+    uint32_t next_;
+    uint32_t state[624];
+} hd_torch_rng;
+
+void hd_torch_rng_seed(hd_torch_rng *rng, uint64_t seed);
+uint32_t hd_torch_rng_u32(hd_torch_rng *rng);
+float hd_torch_uniform_f32(hd_torch_rng *rng);
+/* torch.randn(n) on a CPU generator: n >= 16 uses the 16-wide Box-Muller
+ * fill (last 16 redrawn when n % 16 != 0); n < 16 the double-precision
+ * serial path with a cached second sample. */
+void hd_torch_randn_f32(hd_torch_rng *rng, float *out, int64_t n);
+
+/* ---- scheduler (scheduler.h) ------------------------------------------ */
+#define HD_SCHED_MAX_STEPS 64
+typedef struct {
+    float sigmas[HD_SCHED_MAX_STEPS];
+    int num_steps;          /* sigmas written, including the trailing 0 */
+    int step_index;
+    float noise_clip_std;
+} hd_scheduler;
+
+hd_status hd_scheduler_init(hd_scheduler *s, const float *sigmas, int num_steps,
+                            float noise_clip_std);
+float hd_scheduler_sigma(const hd_scheduler *s);
+/* Dev recipe: the 28 frozen timesteps / 1000 + 0 (scheduler.c:28-72). */
+int hd_scheduler_derive_dev(hd_scheduler *s, float noise_clip_std);
+/* flash / flow_match: ramp in timestep space, shift applied (fp64). */
+int hd_scheduler_derive_flash(hd_scheduler *s, int steps, float shift, float noise_clip_std);
+int hd_scheduler_derive_flow_match(hd_scheduler *s, int steps, float shift,
+                                   float noise_clip_std);
+/* default (UniPC recipe): linear in sigma space, shift applied (fp64). */
+int hd_scheduler_derive_default(hd_scheduler *s, int steps, float shift, float noise_clip_std);
+float hd_scheduler_noise_scale(const hd_scheduler *s, int step_index, float noise_scale_start,
+                               float noise_scale_end);
+/* Flash SDE step on the device (scheduler.c:74-102): upcast z, denoised =
+ * z - mo*sigma, z' = (sigma'*noise)*s_noise + (1-sigma')*denoised -> bf16.
+ * scratch: 3n floats of device memory. */
+hd_status hd_scheduler_step(hd_scheduler *s, const void *z_bf16, const float *model_output,
+                            const float *noise_post_clamp, float s_noise, void *z_next_bf16,
+                            int n, float *scratch);
+
+/* ---- sequence tables (sequence.c:102-142) ------------------------------ */
+/* T2I position ids, pos [3, S] fp32, S = text_len + grid_h*grid_w: text row i
+ * = (i, i, i); image token (r, c) = fix_point + (0, r, c). */
+hd_status hd_seq_t2i_positions(int text_len, int grid_h, int grid_w, int fix_point, float *pos);
+/* [S, S] bf16 additive mask: -max_bf16 (0xFF7F) above the diagonal on rows
+ * < text_len - 1, 0 elsewhere. */
+hd_status hd_seq_t2i_mask(int text_len, int seq, uint16_t *mask);
+/* Synthetic 2-D layout: n_text text rows at (base, base, base), then for each
+ * image segment i a grid_h[i] x grid_w[i] grid at (base, base + row_off[i] + r,
+ * base + col_off[i] + c). Returns the sequence length, or -1. */
+int hd_seq_grid_positions(int n_text, int n_seg, const int *grid_h, const int *grid_w,
+                          const int *row_off, const int *col_off, float base, float *pos);
+
+/* ---- initial latent (generate.c:78-104) -------------------------------- */
+/* randn(3*H*W) from seed + 1, laid out [3, H, W] fp32. */
+void hd_initial_noise(uint64_t seed, int width, int height, float *out);
+/* tok[r*gw + c][ch*p*p + i*p + j] = img[ch][r*p + i][c*p + j] (host). */
+void hd_pixel_unshuffle(const float *img, int channels, int height, int width, int patch,
+                        float *tok);
+/* decode.c:5-27: (v+1)/2*255, round half away from zero, clamp, HWC u8. */
+void hd_decode_to_rgb(const float *z_f32, int grid_h, int grid_w, int patch, int channels,
+                      unsigned char *out);
+
+/* ---- denoising loop (extension; generate.c:1314-1455 restated) ---------
+ * Flow-match Euler with classifier-free guidance, batch 2 in one forward
+ * (row 0 = cond ids, row 1 = uncond ids), all on the device:
+ *   for i in [0, steps):  t = sigma_i for both rows
+ *     x = hd_forward_batched(ids, z, t)               [2, S, 3072]
+ *     mo_c = (z - x_c[img])/sigma_i, mo_u likewise    (hd_sched_vcond)
+ *     mo = (1-g) mo_u + g mo_c                        (hd_sched_cfg_guided)
+ *     z = bf16(z + (sigma_{i+1} - sigma_i) mo)        (hd_sched_flow_match_step)
+ * z: [img_tokens, 3072] bf16, updated in place. sigmas: host, steps + 1.
+ * `ws` must be sized by hd_forward_batched_workspace_bytes(2, ...) and
+ * `scratch` by hd_denoise_scratch_bytes(). */
+int64_t hd_denoise_scratch_bytes(int seq, int img_tokens, int steps);
+hd_status hd_denoise_euler_cfg(const hd_forward_binding *bw, hd_forward_workspace *ws,
+                               const int64_t *ids_dev, int text_len, const float *pos_dev,
+                               int ar_len, void *z_dev, int img_tokens, const float *sigmas,
+                               int steps, float guidance, int seq, int heads, int kv_heads,
+                               int hidden, int ff_hidden, int head_dim, int tms_token_id,
+                               void *scratch, int64_t scratch_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HD_HOST_H */

@@ -549,6 +549,16 @@ extern "C" void hd_scale_f32(const float *in, float *out, float s, int n) {
     scale_kernel<<<hd_cdiv(n, 256), 256, 0, hd_stream()>>>(in, out, s, n);
     hd_check_launch("scale_f32");
 }
+__global__ void fill_kernel(float *dst, float v, int n) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = v;
+}
+// Internal (host.cpp): device fill whose value travels as a kernel argument.
+extern "C" void hd_fill_f32(float *dst, float value, int n) {
+    if (!dst || n <= 0) BAD("fill_f32");
+    fill_kernel<<<hd_cdiv(n, 256), 256, 0, hd_stream()>>>(dst, value, n);
+    hd_check_launch("fill_f32");
+}
 __global__ void cvt_kernel(const float *in, uint16_t *out, int n) {
     int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) out[i] = f2bf(in[i]);

@@ -65,6 +65,16 @@ class hd_forward_diagnostics(ctypes.Structure):
         "before_final_norm", "after_final_norm", "after_final_head")]
 
 
+class hd_torch_rng(ctypes.Structure):
+    _fields_ = [("seed_", ctypes.c_uint64), ("left_", c_int), ("seeded_", c_int),
+                ("next_", ctypes.c_uint32), ("state", ctypes.c_uint32 * 624)]
+
+
+class hd_scheduler(ctypes.Structure):
+    _fields_ = [("sigmas", c_float * 64), ("num_steps", c_int), ("step_index", c_int),
+                ("noise_clip_std", c_float)]
+
+
 class hd_lora_entry(ctypes.Structure):
     _fields_ = [("lora_prefix", ctypes.c_char * 256), ("base_tensor", ctypes.c_char * 256),
                 ("rank", ctypes.c_uint32), ("in_dim", ctypes.c_uint32),
@@ -171,6 +181,29 @@ SIGNATURES = {
                                    c_int, c_int, c_int, c_int, ctypes.POINTER(hd_forward_diagnostics), P, P]),
     # hd_lora.h
     "hd_lora_merge_gpu": (c_int, [ctypes.POINTER(hd_lora_entry), c_size_t, P]),
+    # hd_host.h
+    "hd_torch_rng_seed": (None, [ctypes.POINTER(hd_torch_rng), ctypes.c_uint64]),
+    "hd_torch_rng_u32": (ctypes.c_uint32, [ctypes.POINTER(hd_torch_rng)]),
+    "hd_torch_uniform_f32": (c_float, [ctypes.POINTER(hd_torch_rng)]),
+    "hd_torch_randn_f32": (None, [ctypes.POINTER(hd_torch_rng), P, c_int64]),
+    "hd_scheduler_init": (c_int, [ctypes.POINTER(hd_scheduler), P, c_int, c_float]),
+    "hd_scheduler_sigma": (c_float, [ctypes.POINTER(hd_scheduler)]),
+    "hd_scheduler_derive_dev": (c_int, [ctypes.POINTER(hd_scheduler), c_float]),
+    "hd_scheduler_derive_flash": (c_int, [ctypes.POINTER(hd_scheduler), c_int, c_float, c_float]),
+    "hd_scheduler_derive_flow_match": (c_int, [ctypes.POINTER(hd_scheduler), c_int, c_float, c_float]),
+    "hd_scheduler_derive_default": (c_int, [ctypes.POINTER(hd_scheduler), c_int, c_float, c_float]),
+    "hd_scheduler_noise_scale": (c_float, [ctypes.POINTER(hd_scheduler), c_int, c_float, c_float]),
+    "hd_scheduler_step": (c_int, [ctypes.POINTER(hd_scheduler), P, P, P, c_float, P, c_int, P]),
+    "hd_seq_t2i_positions": (c_int, [c_int, c_int, c_int, c_int, P]),
+    "hd_seq_t2i_mask": (c_int, [c_int, c_int, P]),
+    "hd_seq_grid_positions": (c_int, [c_int, c_int, P, P, P, P, c_float, P]),
+    "hd_initial_noise": (None, [ctypes.c_uint64, c_int, c_int, P]),
+    "hd_pixel_unshuffle": (None, [P, c_int, c_int, c_int, c_int, P]),
+    "hd_decode_to_rgb": (None, [P, c_int, c_int, c_int, c_int, P]),
+    "hd_denoise_scratch_bytes": (c_int64, [c_int, c_int, c_int]),
+    "hd_denoise_euler_cfg": (c_int, [ctypes.POINTER(hd_forward_binding), ctypes.POINTER(hd_forward_workspace),
+                                     P, c_int, P, c_int, P, c_int, P, c_int, c_float, c_int, c_int,
+                                     c_int, c_int, c_int, c_int, c_int, P, c_int64, P]),
 }
 
 _lib = None
@@ -206,6 +239,21 @@ def bind_torch_stream():
 def ptr(t):
     """Device pointer of a torch tensor (None -> NULL)."""
     return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def np_ptr(a):
+    """Host pointer of a contiguous numpy array."""
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def randn(seed, n):
+    """torch CPU randn(n) from manual_seed(seed), via the library's host RNG."""
+    import numpy as np
+    g = hd_torch_rng()
+    load().hd_torch_rng_seed(ctypes.byref(g), seed)
+    out = np.empty(n, np.float32)
+    load().hd_torch_randn_f32(ctypes.byref(g), np_ptr(out), n)
+    return out
 
 
 def check_prim(what=""):
@@ -303,6 +351,9 @@ class SdpaPlan:
             raise RuntimeError(load().hd_cuda_last_error().decode())
 
     def __del__(self):
-        if getattr(self, "h", None) and _lib is not None:
-            _lib.hd_sdpa_destroy(self.h)
-            self.h = None
+        try:
+            if getattr(self, "h", None) and _lib is not None:
+                _lib.hd_sdpa_destroy(self.h)
+                self.h = None
+        except (AttributeError, TypeError):     # interpreter shutdown
+            pass

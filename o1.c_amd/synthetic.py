@@ -68,5 +68,8 @@ class Model:
         H.check_status(st, "hd_forward_resolve")
 
     def __del__(self):
-        if H._lib is not None and getattr(self, "binding", None) is not None:
-            H._lib.hd_forward_binding_free(ctypes.byref(self.binding))
+        try:
+            if H._lib is not None and getattr(self, "binding", None) is not None:
+                H._lib.hd_forward_binding_free(ctypes.byref(self.binding))
+        except (AttributeError, TypeError):     # interpreter shutdown
+            pass

@@ -6,6 +6,9 @@ Sources (nothing here imports or runs reference code):
     exact integer arithmetic, then bf16 round-to-nearest-even).
   * positions_s23.json - the position-id known answer quoted in
     src/runtime/sequence.c:97-100 (S=23, T=19, 2x2 grid, fix point 4096).
+  * scheduler_sigmas.json - the SIGMAS rows of the reference's scheduler
+    oracle dump (tests/unit/oracle_dump.txt: recipe name, steps, shift,
+    scheduler kind, sigmas), produced upstream by the Python pipeline.
   * bf16_rne.json - bf16 RNE bit patterns of seeded float32 values produced
     by torch (the library whose conversion the reference emulates,
     support.cu:21-28), including ties and subnormals.
@@ -67,9 +70,25 @@ def bf16_rne():
             "f32_bits": [b & 0xFFFFFFFF for b in bits_in], "bf16_bits": out}
 
 
+def scheduler_sigmas(path="/root/reference/tests/unit/oracle_dump.txt"):
+    recipes = []
+    cur = None
+    for line in open(path):
+        parts = line.split()
+        if not parts:
+            continue
+        if parts[0] == "RECIPE":
+            cur = {"name": parts[1], "steps": int(parts[2]), "shift": float(parts[3]),
+                   "kind": parts[4], "explicit_timesteps": parts[5] == "True"}
+            recipes.append(cur)
+        elif parts[0] == "SIGMAS" and cur is not None:
+            cur["sigmas"] = [float(v) for v in parts[1:]]
+    return {"source": "tests/unit/oracle_dump.txt (RECIPE/SIGMAS rows)", "recipes": recipes}
+
+
 if __name__ == "__main__":
     for name, fn in (("gemm_smoke.json", gemm_smoke), ("positions_s23.json", positions),
-                     ("bf16_rne.json", bf16_rne)):
+                     ("bf16_rne.json", bf16_rne), ("scheduler_sigmas.json", scheduler_sigmas)):
         with open(os.path.join(HERE, name), "w") as f:
             json.dump(fn(), f, indent=1)
         print("wrote", name)

@@ -154,3 +154,96 @@ def test_forward_batched_matches_single(pkg, lib, dev):
         torch.cuda.synchronize()
         # same kernels, M differs (B*S vs S rows): GEMM tiles differ -> a few ulps
         assert rel_l2(out[b].float().cpu(), o1.float().cpu()) < 5e-3
+
+
+def test_denoise_loop_matches_stepwise(pkg, lib, dev):
+    """hd_denoise_euler_cfg (device loop): (1) one step equals the step
+    composed by hand from hd_forward_batched + the sampler formulas
+    (sched.cu:50-72, :137-145) up to division/fma rounding; (2) a 3-step loop
+    equals three chained 1-step loops bit for bit (guidance 5 and 1/sigma
+    amplify any single-ulp difference chaotically, so multi-step agreement
+    with a restatement is not a meaningful bound)."""
+    import importlib
+    synth = importlib.import_module("o1c_amd.synthetic")
+    nL, HID, H, KV, FF, D = 1, 512, 4, 2, 1024, 128
+    T, gh, gw = 16, 8, 8
+    I = gh * gw
+    S = T + I
+    tens = synth.build_model(n_layers=nL, hidden=HID, heads=H, kv_heads=KV, ff=FF, seed=9)
+    model = synth.Model(tens, nL)
+    pkg.set_block_config(theta=1e4)
+    posd = torch.from_numpy(grid_pos(T, gh, gw)).to(dev)
+    g = torch.Generator().manual_seed(2)
+    ids = torch.randint(0, 151643, (2, T), generator=g)
+    ids[:, -1] = TMS
+    idsd = ids.to(dev)
+    z0 = torch.randn(I, 3072, generator=g).to(dev, torch.bfloat16)
+    sch = pkg.hd_scheduler()
+    steps = 3
+    n = lib.hd_scheduler_derive_default(ctypes.byref(sch), steps, 3.0, 8.0)
+    sig = [sch.sigmas[i] for i in range(n)]
+    wsb = lib.hd_forward_batched_workspace_bytes(2, S, I, H, KV, HID, FF, D)
+    buf = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    ws = pkg.hd_forward_workspace()
+    ws.hidden_a = buf.data_ptr()
+    sb = lib.hd_denoise_scratch_bytes(S, I, steps)
+    scratch = torch.empty(sb, dtype=torch.uint8, device=dev)
+
+    def loop(z, sigmas):
+        k = len(sigmas) - 1
+        st = lib.hd_denoise_euler_cfg(ctypes.byref(model.binding), ctypes.byref(ws), pkg.ptr(idsd),
+                                      T, pkg.ptr(posd), 0, pkg.ptr(z), I,
+                                      (ctypes.c_float * len(sigmas))(*sigmas), k, 5.0, S, H, KV,
+                                      HID, FF, D, TMS, pkg.ptr(scratch), sb, None)
+        pkg.check_status(st, "denoise")
+
+    z3 = z0.clone()
+    loop(z3, sig)
+    zc = z0.clone()
+    for i in range(steps):
+        loop(zc, sig[i:i + 2])
+    torch.cuda.synchronize()
+    assert torch.equal(z3, zc)
+    assert float((z3.float() - z0.float()).abs().mean()) > 1e-3      # the latent moved
+    # one step by hand
+    z1 = z0.clone()
+    loop(z1, sig[:2])
+    out = torch.empty(2, S, 3072, dtype=torch.bfloat16, device=dev)
+    vin = z0.unsqueeze(0).repeat(2, 1, 1).contiguous()
+    td = torch.full((2,), sig[0], dtype=torch.float32, device=dev)
+    st = lib.hd_forward_batched(ctypes.byref(model.binding), ctypes.byref(ws), 2, pkg.ptr(idsd), T,
+                                pkg.ptr(posd), 0, pkg.ptr(vin), I, pkg.ptr(td), S, H, KV, HID, FF,
+                                D, TMS, None, pkg.ptr(out), None)
+    pkg.check_status(st, "forward")
+    zf = z0.float()
+    s32 = torch.tensor(sig[0], dtype=torch.float32)
+    mo_c = (zf - out[0, T:].float()) / s32
+    mo_u = (zf - out[1, T:].float()) / s32
+    mo = (5.0 * mo_c.double() + ((1.0 - 5.0) * mo_u).double()).float()      # fma(g, c, (1-g) u)
+    dt = float(np.float32(sig[1]) - np.float32(sig[0]))
+    zr = (zf.double() + dt * mo.double()).float().to(torch.bfloat16)       # bf16(fma(dt, mo, z))
+    torch.cuda.synchronize()
+    assert rel_l2(z1.float().cpu(), zr.float().cpu()) < 2e-3
+    assert (z1 == zr).float().mean().item() > 0.99
+
+
+def test_scheduler_step_device(pkg, lib, dev):
+    sch = pkg.hd_scheduler()
+    lib.hd_scheduler_derive_flash(ctypes.byref(sch), 28, 1.0, 8.0)
+    n = 4096
+    g = torch.Generator().manual_seed(4)
+    z = torch.randn(n, generator=g).to(dev, torch.bfloat16)
+    mo = torch.randn(n, generator=g).to(dev)
+    noise = torch.randn(n, generator=g).to(dev)
+    zn = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    scratch = torch.empty(3 * n, device=dev)
+    st = lib.hd_scheduler_step(ctypes.byref(sch), pkg.ptr(z), pkg.ptr(mo), pkg.ptr(noise), 1.0,
+                               pkg.ptr(zn), n, pkg.ptr(scratch))
+    pkg.check_status(st, "step")
+    assert sch.step_index == 1
+    sg, sn = np.float32(sch.sigmas[0]), np.float32(sch.sigmas[1])
+    zf = z.float().cpu().double()
+    den = (zf - mo.cpu().double() * sg).float()                       # fma(-mo, sigma, z)
+    want = ((noise.cpu().double() * sn).float().double() + (1 - sn) * den.double()).float()
+    want = want.to(torch.bfloat16).float()
+    assert rel_l2(zn.float().cpu(), want) < 3e-3
