@@ -294,7 +294,8 @@ template <int CPR> __device__ __forceinline__ int ms_swz(int r) {
     return CPR == 8 ? ((r >> 1) & 7) : ((r >> 2) & 3);
 }
 
-template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 0, int OCC = 1>
+template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 0, int OCC = 1,
+          int LDR = 0>
 __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g) {
     using C = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI>;
     constexpr int WTM = C::WTM, WTN = C::WTN, TM = C::TM, TN = C::TN, CPR = C::CPR;
@@ -332,10 +333,14 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
             n = min(n, g.N - 1);
             p = (j < WTN / 2 ? g.B[0] : g.B[1]) + (size_t)n * g.K;
         } else {
-            int n = min(tn * BN + r, g.seg_end[2] - 1);
-            int sg = n < g.seg_end[0] ? 0 : (n < g.seg_end[1] ? 1 : 2);
-            int base = sg == 0 ? 0 : g.seg_end[sg - 1];
-            p = g.B[sg] + (size_t)(n - base) * g.K;
+            // a 256-aligned column tile lies in one weight segment (q/k/v)
+            const int t0 = tn * BN;
+            const int sg = t0 < g.seg_end[0] ? 0 : (t0 < g.seg_end[1] ? 1 : 2);
+            const uint16_t *bp = sg == 0 ? g.B[0] : (sg == 1 ? g.B[1] : g.B[2]);
+            const int base = sg == 0 ? 0 : (sg == 1 ? g.seg_end[0] : g.seg_end[1]);
+            const int last = (sg == 0 ? g.seg_end[0] : (sg == 1 ? g.seg_end[1] : g.seg_end[2])) - 1;
+            int n = min(t0 + r, last);
+            p = bp + (size_t)(n - base) * g.K;
         }
         b_src[i] = p + (cl ^ ms_swz<CPR>(r)) * 8;
     }
@@ -350,6 +355,22 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
             __builtin_amdgcn_global_load_lds((const void *)(b_src[i] + kt * BK),
                                              (HD_LDS void *)(Bs + (wave * BI + i) * 512), 16, 0, 0);
     };
+    // LDR 1: the same chunks through registers (global_load_dwordx4 then
+    // ds_write_b128 at the swizzled slot), each lane keeping its rows.
+    u32x4_t ra[AI], rb[BI];
+    auto gload = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < AI; i++) ra[i] = *(const u32x4_t *)(a_src[i] + kt * BK);
+#pragma unroll
+        for (int i = 0; i < BI; i++) rb[i] = *(const u32x4_t *)(b_src[i] + kt * BK);
+    };
+    auto lstore = [&](int st) {
+        uint16_t *As = smem + st * C::STAGE, *Bs = As + BM * BK;
+#pragma unroll
+        for (int i = 0; i < AI; i++) *(u32x4_t *)(As + (wave * AI + i) * 512 + lane * 8) = ra[i];
+#pragma unroll
+        for (int i = 0; i < BI; i++) *(u32x4_t *)(Bs + (wave * BI + i) * 512 + lane * 8) = rb[i];
+    };
 
     f32x16_t acc[TM][TN];
 #pragma unroll
@@ -362,14 +383,27 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
     const int nk = g.K / BK;
     const int l32 = lane & 31, khalf = lane >> 5;
     const int sw = ms_swz<CPR>(l32);
+    if (LDR) {
+        // 2-stage ring through registers: load k+1 early, store it after the
+        // MFMAs of k, one barrier per K tile
+        gload(0);
+        lstore(0);
+        __syncthreads();
+    }
+    if (!LDR) {
 #pragma unroll
-    for (int s = 0; s < NS - 1; s++)
-        if (s < nk) issue(s, s);
+        for (int s = 0; s < NS - 1; s++)
+            if (s < nk) issue(s, s);
+    }
     for (int kt = 0; kt < nk; kt++) {
-        if (kt + NS - 2 < nk) wait_vm_barrier<(NS - 2) * C::LPT>();
-        else wait_vm_barrier<0>();
-        if (kt + NS - 1 < nk) issue(kt + NS - 1, (kt + NS - 1) % NS);
-        const uint16_t *As = smem + (kt % NS) * C::STAGE, *Bs = As + BM * BK;
+        if (LDR) {
+            if (kt + 1 < nk) gload(kt + 1);
+        } else {
+            if (kt + NS - 2 < nk) wait_vm_barrier<(NS - 2) * C::LPT>();
+            else wait_vm_barrier<0>();
+            if (kt + NS - 1 < nk) issue(kt + NS - 1, (kt + NS - 1) % NS);
+        }
+        const uint16_t *As = smem + (LDR ? (kt & 1) : (kt % NS)) * C::STAGE, *Bs = As + BM * BK;
         if (SGB) {
             // register double buffer of fragments; the reads of k-step ks+1
             // are interleaved one by one with the MFMAs of ks (SGB 2: the
@@ -424,6 +458,10 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[j], af[i], acc[i][j], 0, 0, 0);
         }
         }
+        if (LDR) {
+            if (kt + 1 < nk) lstore((kt + 1) & 1);
+            __syncthreads();
+        }
     }
     __syncthreads();   // every wave is done with the ring before staging reuses it
 
@@ -458,6 +496,198 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
     constexpr int CPRO = WO / 8, RPIO = 64 / CPRO;
     const int gm0 = m0 + wm * WTM;
     const int gn0 = tn * C::BN_OUT + wn * WO;
+#pragma unroll 4
+    for (int r0 = 0; r0 < WTM; r0 += RPIO) {
+        const int r = r0 + lane / CPRO, cc = (lane % CPRO) * 8;
+        const int m = gm0 + r, n = gn0 + cc;
+        if (m < g.M && n < g.N) {
+            u32x4_t v = *(const u32x4_t *)(stg + r * LDW + cc);
+            if (EPI == EPI_BIAS || EPI == EPI_RES) {
+                u32x4_t o = EPI == EPI_BIAS ? *(const u32x4_t *)(g.bias + n)
+                                            : *(const u32x4_t *)(g.res + (size_t)m * g.ldc + n);
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    v[e] = pack_bf2(lo_bf(v[e]) + lo_bf(o[e]), hi_bf(v[e]) + hi_bf(o[e]));
+            }
+            *(u32x4_t *)(g.C + (size_t)m * g.ldc + n) = v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Ping-pong variant: 8 waves in two groups of 4 (one wave of each group per
+// SIMD). Group 0 owns output rows [0, BM/2), group 1 rows [BM/2, BM); each
+// wave a (BM/2) x 64 slice. The groups run one phase apart:
+//   phase 2t   : group 0 reads the fragments of K tile t from LDS into
+//                registers and issues the global->LDS loads of tile t+1;
+//                group 1 runs the MFMAs of tile t-1
+//   phase 2t+1 : group 0 runs the MFMAs of tile t (then waits for tile t+1);
+//                group 1 reads the fragments of tile t
+// with one workgroup barrier between phases, so on every SIMD one wave feeds
+// the matrix core while its partner does memory work. LDS: two 64-deep
+// stages; a stage is rewritten only after both groups have read it.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void pp_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int BM, int EPI>
+__global__ __launch_bounds__(512) void gemm_pp_kernel(GemmArgs g) {
+    constexpr int BN = 256, BK = 64, NW = 8;
+    constexpr int WTM = BM / 2, WTN = 64, TM = WTM / 32, TN = 2;
+    constexpr int STAGE = (BM + BN) * BK;
+    constexpr int WTN_OUT = EPI == EPI_SWIGLU ? WTN / 2 : WTN;
+    constexpr int BN_OUT = EPI == EPI_SWIGLU ? BN / 2 : BN;
+    constexpr int EPAD = 8, LDW = WTN_OUT + EPAD;
+    constexpr int MAIN_BYTES = 2 * STAGE * 2, EPI_BYTES = NW * WTM * LDW * 2;
+    constexpr int LDS_BYTES = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
+    constexpr int AI = BM / 8 / 4, BI = BN / 8 / 4;   // loads per group-0 wave
+    constexpr int GROUP_M = 8;
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[LDS_BYTES / 2];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = wave >> 2, wn = wave & 3;
+    const int nblk = g.ntm * g.ntn;
+    const int lin = xcd_remap(blockIdx.x, nblk);
+    const int in_group = GROUP_M * g.ntn;
+    const int first_m = (lin / in_group) * GROUP_M;
+    const int gm = min(g.ntm - first_m, GROUP_M);
+    const int tm = first_m + (lin % in_group) % gm;
+    const int tn = (lin % in_group) / gm;
+    const int m0 = tm * BM;
+
+    // group-0 waves own the global->LDS traffic of whole tiles; the source
+    // addresses are recomputed per tile (cheap in the memory phase, and it
+    // keeps 16 64-bit pointers out of the register budget)
+    const int sub = lane >> 3, cl = lane & 7;
+    const int lw = wave & 3;
+    // weight segments (q/k/v) are multiples of 256 rows: a column tile lies
+    // in one segment, chosen once per block (scalar)
+    const int tile_n0 = __builtin_amdgcn_readfirstlane(tn * BN);
+    const int seg = tile_n0 < g.seg_end[0] ? 0 : (tile_n0 < g.seg_end[1] ? 1 : 2);
+    const uint16_t *seg_ptr = seg == 0 ? g.B[0] : (seg == 1 ? g.B[1] : g.B[2]);
+    const int seg_base = seg == 0 ? 0 : (seg == 1 ? g.seg_end[0] : g.seg_end[1]);
+    const int seg_last = (seg == 0 ? g.seg_end[0] : (seg == 1 ? g.seg_end[1] : g.seg_end[2])) - 1;
+    auto issue = [&](int kt, int st) {
+        uint16_t *As = smem + st * STAGE, *Bs = As + BM * BK;
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int i = 0; i < AI; i++) {
+            const int r = (lw * AI + i) * 8 + sub;
+            const int m = min(m0 + r, g.M - 1);
+            const uint16_t *src = g.A + (size_t)m * g.K + k0 + (cl ^ ms_swz<8>(r)) * 8;
+            __builtin_amdgcn_global_load_lds((const void *)src,
+                                             (HD_LDS void *)(As + (lw * AI + i) * 512), 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < BI; i++) {
+            const int r = (lw * BI + i) * 8 + sub;
+            const uint16_t *p;
+            if (EPI == EPI_SWIGLU) {
+                const int gq = r / WTN, j = r % WTN;
+                const int n = min(tn * BN_OUT + gq * (WTN / 2) + (j % (WTN / 2)), g.N - 1);
+                p = (j < WTN / 2 ? g.B[0] : g.B[1]) + (size_t)n * g.K;
+            } else {
+                const int n = min(tn * BN + r, seg_last);
+                p = seg_ptr + (size_t)(n - seg_base) * g.K;
+            }
+            __builtin_amdgcn_global_load_lds((const void *)(p + k0 + (cl ^ ms_swz<8>(r)) * 8),
+                                             (HD_LDS void *)(Bs + (lw * BI + i) * 512), 16, 0, 0);
+        }
+    };
+
+    f32x16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    const int l32 = lane & 31, khalf = lane >> 5;
+    const int sw = ms_swz<8>(l32);
+    // one phase = half a K tile (2 k-steps): 16 MFMAs, 12 fragment reads
+    bf16x8_t af[2][TM], bw[2][TN];
+    auto frags = [&](int h) {
+        const uint16_t *As = smem + ((h >> 1) & 1) * STAGE, *Bs = As + BM * BK;
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+            const int ks = (h & 1) * 2 + kk;
+            const int c = ((ks * 2 + khalf) ^ sw) * 8;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                af[kk][i] = *(const bf16x8_t *)(As + (grp * WTM + i * 32 + l32) * BK + c);
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                bw[kk][j] = *(const bf16x8_t *)(Bs + (wn * WTN + j * 32 + l32) * BK + c);
+        }
+    };
+    auto mfmas = [&]() {
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[kk][j], af[kk][i], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_s_setprio(0);
+    };
+
+    const int nk = g.K / BK, NH = 2 * nk;
+    if (grp == 0) {
+        issue(0, 0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    pp_barrier();
+    // Both groups run the same (memory | barrier | MFMA | barrier) loop over
+    // half tiles; group 1 starts one barrier later and group 0 ends with
+    // one extra, so barrier k pairs group 0's MFMA phase with group 1's
+    // memory phase and vice versa. Group 0 requests K tile t+1 while reading
+    // the first half of tile t and waits for it after its MFMAs on the
+    // second half (four phases of latency).
+    if (grp == 1) pp_barrier();
+    for (int h = 0; h < NH; h++) {
+        const int t = h >> 1;
+        frags(h);
+        if (grp == 0 && (h & 1) == 0 && t + 1 < nk) issue(t + 1, (t + 1) & 1);
+        pp_barrier();
+        mfmas();
+        if (grp == 0 && (h & 1) == 1 && t + 1 < nk) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        pp_barrier();
+    }
+    if (grp == 0) pp_barrier();
+    __syncthreads();
+
+    uint16_t *stg = smem + wave * WTM * LDW;
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        const int row = i * 32 + l32;
+#pragma unroll
+        for (int j = 0; j < (EPI == EPI_SWIGLU ? TN / 2 : TN); j++) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float x = acc[i][j][q * 4 + e];
+                    if (EPI == EPI_SWIGLU) {
+                        float gt = bfround(x);
+                        float up = bfround(acc[i][j + TN / 2][q * 4 + e]);
+                        float sgm = bfround(gt * (1.0f / (1.0f + __expf(-gt))));
+                        x = sgm * up;
+                    }
+                    v[e] = x;
+                }
+                const int col = j * 32 + q * 8 + khalf * 4;
+                u32x2_t pk = {pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+                *(u32x2_t *)(stg + row * LDW + col) = pk;
+            }
+        }
+    }
+    __syncthreads();
+    constexpr int CPRO = WTN_OUT / 8, RPIO = 64 / CPRO;
+    const int gm0 = m0 + grp * WTM;
+    const int gn0 = tn * BN_OUT + wn * WTN_OUT;
 #pragma unroll 4
     for (int r0 = 0; r0 < WTM; r0 += RPIO) {
         const int r = r0 + lane / CPRO, cc = (lane % CPRO) * 8;
@@ -549,12 +779,21 @@ static void launch_cfg(GemmArgs &g) {
         <<<g.ntm * g.ntn, Cfg::NT, 0, hd_stream()>>>(g);
 }
 
-template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 0, int OCC = 1>
+template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 0, int OCC = 1,
+          int LDR = 0>
 static void launch_ms(GemmArgs &g) {
     using Cfg = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI>;
     g.ntm = (g.M + BM - 1) / BM;
     g.ntn = (g.N + Cfg::BN_OUT - 1) / Cfg::BN_OUT;
-    gemm_ms_kernel<BM, BN, BK, NS, WGM, WGN, EPI, SGB, OCC><<<g.ntm * g.ntn, Cfg::NT, 0, hd_stream()>>>(g);
+    gemm_ms_kernel<BM, BN, BK, NS, WGM, WGN, EPI, SGB, OCC, LDR>
+        <<<g.ntm * g.ntn, Cfg::NT, 0, hd_stream()>>>(g);
+}
+
+template <int BM, int EPI>
+static void launch_pp(GemmArgs &g) {
+    g.ntm = (g.M + BM - 1) / BM;
+    g.ntn = (g.N + (EPI == EPI_SWIGLU ? 128 : 256) - 1) / (EPI == EPI_SWIGLU ? 128 : 256);
+    gemm_pp_kernel<BM, EPI><<<g.ntm * g.ntn, 512, 0, hd_stream()>>>(g);
 }
 
 // Tuning table: every configuration that hd_gemm_tune_run can launch.
@@ -578,6 +817,12 @@ static bool run_table(int cfg, GemmArgs &g) {
     case 16: launch_ms<256, 128, 32, 3, 2, 2, EPI, 2, 2>(g); return true;
     case 17: launch_ms<192, 128, 32, 3, 2, 2, EPI, 1, 2>(g); return true;
     case 18: launch_ms<128, 128, 64, 2, 2, 2, EPI, 1, 2>(g); return true;
+    case 19: launch_pp<256, EPI>(g); return true;                           // ping-pong
+    case 20: launch_pp<192, EPI>(g); return true;
+    case 21: launch_ms<256, 256, 64, 2, 2, 4, EPI, 1, 1, 1>(g); return true;  // register loader
+    case 22: launch_ms<256, 256, 64, 2, 2, 4, EPI, 0, 1, 1>(g); return true;
+    case 23: launch_ms<192, 256, 64, 2, 2, 4, EPI, 1, 1, 1>(g); return true;
+    case 24: launch_ms<256, 256, 64, 2, 2, 2, EPI, 1, 1, 1>(g); return true;
     case 7: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 1>(g); return true;    // diag: compute only
     case 8: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 2>(g); return true;    // diag: loads only
     default: return false;
