@@ -69,7 +69,7 @@ void hd_linear_concat3(const void *x_dev, const void *w0, int N0,
                        const void *w1, int N1, const void *w2, int N2,
                        void *y_dev, int M, int K);
 
-/* Diagnostics/tuning: launches tuning-table configuration `cfg` (0..8)
+/* Diagnostics/tuning: launches tuning-table configuration `cfg` (0..35)
  * with epilogue 0 (plain, N outputs) or 3 (SwiGLU: w0 = gate, w1 = up, N =
  * F outputs). Returns 0 when launched, non-zero for an unknown config or
  * unsupported shape. */
@@ -79,6 +79,11 @@ int hd_gemm_tune_run(int cfg, int epi, const void *x, const void *w0, const void
 /* Name of the kernel configuration hd_linear* would launch for a shape
  * (diagnostics; static string). */
 const char *hd_gemm_config_name(int M, int N, int K, int epilogue);
+
+/* Diagnostics/tuning: kernel family for the production GEMMs. 0 (default):
+ * 4-wave fragment-ring tiles for K <= 8192, 8-wave interleaved tiles above;
+ * 1: 8-wave interleaved tiles for every shape. Returns the previous value. */
+int hd_gemm_set_family(int family);
 
 #ifdef __cplusplus
 }

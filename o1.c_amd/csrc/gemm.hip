@@ -20,6 +20,7 @@
 #include <stdlib.h>
 #include <string.h>
 #include <math.h>
+#include <type_traits>
 
 #include "hd_common.hpp"
 #include "../../include/hd_hip.h"
@@ -268,10 +269,17 @@ template <int N> __device__ __forceinline__ void wait_vm_barrier() {
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI>
+// as above, and the wave's own LDS reads have completed (the barrier then
+// also means no wave still reads the stage about to be refilled)
+template <int N> __device__ __forceinline__ void wait_lgk_vm_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int MF = 32>
 struct MsCfg {
     static constexpr int NW = WGM * WGN, NT = NW * 64;
-    static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
+    static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / MF, TN = WTN / MF;
     static constexpr int WTN_OUT = EPI == EPI_SWIGLU ? WTN / 2 : WTN;
     static constexpr int BN_OUT = EPI == EPI_SWIGLU ? BN / 2 : BN;
     static constexpr int CPR = BK / 8;            // 16-byte chunks per tile row
@@ -295,9 +303,13 @@ template <int CPR> __device__ __forceinline__ int ms_swz(int r) {
 }
 
 template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 0, int OCC = 1,
-          int LDR = 0>
+          int LDR = 0, int MF = 32>
 __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g) {
-    using C = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI>;
+    // MF: MFMA shape, 32 (v_mfma_f32_32x32x16_bf16) or 16 (16x16x32, SGB 3 only)
+    static_assert(MF == 32 || SGB == 3, "16x16 MFMA tiles use the continuous ring");
+    using C = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI, MF>;
+    using AccT = typename std::conditional<MF == 32, f32x16_t, f32x4_t>::type;
+    constexpr int ACCN = MF == 32 ? 16 : 4;
     constexpr int WTM = C::WTM, WTN = C::WTN, TM = C::TM, TN = C::TN, CPR = C::CPR;
     constexpr int AI = C::AI, BI = C::BI, GROUP_M = 8;
     __shared__ __attribute__((aligned(1024))) uint16_t smem[C::LDS_BYTES / 2];
@@ -344,15 +356,18 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
         }
         b_src[i] = p + (cl ^ ms_swz<CPR>(r)) * 8;
     }
+    // LDR 2 (diagnostic): every K tile re-reads tile 0, so all loads hit in
+    // cache and the instruction stream is otherwise unchanged
+    auto koff = [&](int kt) { return LDR == 2 ? 0 : kt * BK; };
     auto issue = [&](int kt, int st) {
         uint16_t *As = smem + st * C::STAGE, *Bs = As + BM * BK;
 #pragma unroll
         for (int i = 0; i < AI; i++)
-            __builtin_amdgcn_global_load_lds((const void *)(a_src[i] + kt * BK),
+            __builtin_amdgcn_global_load_lds((const void *)(a_src[i] + koff(kt)),
                                              (HD_LDS void *)(As + (wave * AI + i) * 512), 16, 0, 0);
 #pragma unroll
         for (int i = 0; i < BI; i++)
-            __builtin_amdgcn_global_load_lds((const void *)(b_src[i] + kt * BK),
+            __builtin_amdgcn_global_load_lds((const void *)(b_src[i] + koff(kt)),
                                              (HD_LDS void *)(Bs + (wave * BI + i) * 512), 16, 0, 0);
     };
     // LDR 1: the same chunks through registers (global_load_dwordx4 then
@@ -372,38 +387,115 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
         for (int i = 0; i < BI; i++) *(u32x4_t *)(Bs + (wave * BI + i) * 512 + lane * 8) = rb[i];
     };
 
-    f32x16_t acc[TM][TN];
+    AccT acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+            for (int r = 0; r < ACCN; r++) acc[i][j][r] = 0.f;
 
     const int nk = g.K / BK;
     const int l32 = lane & 31, khalf = lane >> 5;
     const int sw = ms_swz<CPR>(l32);
-    if (LDR) {
+    if constexpr (SGB == 3) {
+        // One fragment ring across the whole K loop (one wave per SIMD has no
+        // partner wave to cover a refill bubble): the fragments of k-step
+        // ks+1 load under the MFMAs of ks, and at the last k-step of a tile
+        // the barrier, the refill of the stage just read and the first
+        // fragments of the next tile all go under that k-step's MFMAs.
+        // k-steps per tile: 16 deep (32x32x16) or 32 deep (16x16x32); a lane
+        // reads 8 consecutive k of row lane % MF, chunk lane / MF of the step
+        constexpr int KS = BK / (MF == 32 ? 16 : 32), NR = TM + TN, NM = TM * TN, LPT = C::LPT;
+        constexpr int CPS = 64 / MF;   // 16-byte chunks per k-step
+        static_assert(KS % 2 == 0, "fragment slots");
+        const int lr = lane % MF, lc = lane / MF, swr = ms_swz<CPR>(lr);
+        bf16x8_t af[2][TM], bw[2][TN];
+        auto ld = [&](const uint16_t *As, int ks, int sl) {
+            const uint16_t *Bs = As + BM * BK;
+            const int c = ((ks * CPS + lc) ^ swr) * 8;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                af[sl][i] = *(const bf16x8_t *)(As + (wm * WTM + i * MF + lr) * BK + c);
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                bw[sl][j] = *(const bf16x8_t *)(Bs + (wn * WTN + j * MF + lr) * BK + c);
+        };
+#pragma unroll
+        for (int st = 0; st < NS; st++)
+            if (st < nk) issue(st, st);
+        if (nk >= NS) wait_vm_barrier<(NS - 1) * LPT>();
+        else wait_vm_barrier<0>();
+        ld(smem, 0, 0);
+        // REFILL: tile kt+NS exists; NEXT: tile kt+1 exists. Compile-time
+        // flags keep the steady-state body free of branches, so the MFMA /
+        // load / read interleave below survives scheduling.
+        auto tile = [&](int kt, auto refill, auto next) {
+            constexpr bool REFILL = decltype(refill)::value, NEXT = decltype(next)::value;
+            const uint16_t *As = smem + (kt % NS) * C::STAGE;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                const bool last = ks + 1 == KS;
+                if (!last) {
+                    ld(As, ks + 1, (ks + 1) & 1);
+                } else {
+                    // tile kt+1 has landed and every wave is done reading
+                    // stage kt % NS (its last fragments are in registers)
+                    if (REFILL) wait_lgk_vm_barrier<(NS - 2) * LPT>();
+                    else wait_lgk_vm_barrier<0>();
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (REFILL) issue(kt + NS, kt % NS);
+                    if (NEXT) ld(smem + ((kt + 1) % NS) * C::STAGE, 0, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++) {
+                        if constexpr (MF == 32)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[ks & 1][j], af[ks & 1][i],
+                                                                                 acc[i][j], 0, 0, 0);
+                        else
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bw[ks & 1][j], af[ks & 1][i],
+                                                                                 acc[i][j], 0, 0, 0);
+                    }
+                const int nv = last && REFILL ? LPT : 0;
+                const int nr = !last || NEXT ? NR : 0;
+#pragma unroll
+                for (int q = 0; q < NM; q++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    if (q < nv) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                    if (q < nr) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+            }
+        };
+        using T_ = std::true_type;
+        using F_ = std::false_type;
+        int kt = 0;
+        for (; kt + NS < nk; kt++) tile(kt, T_{}, T_{});
+        for (; kt + 1 < nk; kt++) tile(kt, F_{}, T_{});
+        tile(kt, F_{}, F_{});
+    } else {
+    if (LDR == 1) {
         // 2-stage ring through registers: load k+1 early, store it after the
         // MFMAs of k, one barrier per K tile
         gload(0);
         lstore(0);
         __syncthreads();
     }
-    if (!LDR) {
+    if (LDR != 1) {
 #pragma unroll
         for (int s = 0; s < NS - 1; s++)
             if (s < nk) issue(s, s);
     }
     for (int kt = 0; kt < nk; kt++) {
-        if (LDR) {
+        if (LDR == 1) {
             if (kt + 1 < nk) gload(kt + 1);
         } else {
             if (kt + NS - 2 < nk) wait_vm_barrier<(NS - 2) * C::LPT>();
             else wait_vm_barrier<0>();
             if (kt + NS - 1 < nk) issue(kt + NS - 1, (kt + NS - 1) % NS);
         }
-        const uint16_t *As = smem + (LDR ? (kt & 1) : (kt % NS)) * C::STAGE, *Bs = As + BM * BK;
+        const uint16_t *As = smem + (LDR == 1 ? (kt & 1) : (kt % NS)) * C::STAGE, *Bs = As + BM * BK;
         if (SGB) {
             // register double buffer of fragments; the reads of k-step ks+1
             // are interleaved one by one with the MFMAs of ks (SGB 2: the
@@ -458,22 +550,27 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[j], af[i], acc[i][j], 0, 0, 0);
         }
         }
-        if (LDR) {
+        if (LDR == 1) {
             if (kt + 1 < nk) lstore((kt + 1) & 1);
             __syncthreads();
         }
+    }
     }
     __syncthreads();   // every wave is done with the ring before staging reuses it
 
     constexpr int WO = C::WTN_OUT, LDW = WO + C::EPAD;
     uint16_t *stg = smem + wave * WTM * LDW;
+    // a lane holds, per accumulator, runs of 4 consecutive output columns:
+    // 32x32: columns q*8 + khalf*4 (q < 4) of row lane % 32;
+    // 16x16: columns (lane / 16)*4 of row lane % 16
+    constexpr int NQ = MF == 32 ? 4 : 1;
 #pragma unroll
     for (int i = 0; i < TM; i++) {
-        const int row = i * 32 + l32;
+        const int row = i * MF + (MF == 32 ? l32 : (lane & 15));
 #pragma unroll
         for (int j = 0; j < (EPI == EPI_SWIGLU ? TN / 2 : TN); j++) {
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
+            for (int q = 0; q < NQ; q++) {
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
@@ -486,7 +583,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
                     }
                     v[e] = x;
                 }
-                const int col = j * 32 + q * 8 + khalf * 4;
+                const int col = MF == 32 ? j * 32 + q * 8 + khalf * 4 : j * 16 + (lane >> 4) * 4;
                 u32x2_t pk = {pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
                 *(u32x2_t *)(stg + row * LDW + col) = pk;
             }
@@ -780,12 +877,12 @@ static void launch_cfg(GemmArgs &g) {
 }
 
 template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 0, int OCC = 1,
-          int LDR = 0>
+          int LDR = 0, int MF = 32>
 static void launch_ms(GemmArgs &g) {
-    using Cfg = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI>;
+    using Cfg = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI, MF>;
     g.ntm = (g.M + BM - 1) / BM;
     g.ntn = (g.N + Cfg::BN_OUT - 1) / Cfg::BN_OUT;
-    gemm_ms_kernel<BM, BN, BK, NS, WGM, WGN, EPI, SGB, OCC, LDR>
+    gemm_ms_kernel<BM, BN, BK, NS, WGM, WGN, EPI, SGB, OCC, LDR, MF>
         <<<g.ntm * g.ntn, Cfg::NT, 0, hd_stream()>>>(g);
 }
 
@@ -823,6 +920,17 @@ static bool run_table(int cfg, GemmArgs &g) {
     case 22: launch_ms<256, 256, 64, 2, 2, 4, EPI, 0, 1, 1>(g); return true;
     case 23: launch_ms<192, 256, 64, 2, 2, 4, EPI, 1, 1, 1>(g); return true;
     case 24: launch_ms<256, 256, 64, 2, 2, 2, EPI, 1, 1, 1>(g); return true;
+    case 25: launch_ms<256, 256, 64, 2, 2, 2, EPI, 1>(g); return true;       // 4 waves 128x128
+    case 26: launch_ms<256, 256, 64, 2, 2, 2, EPI, 3>(g); return true;       // 4 waves, continuous ring
+    case 27: launch_ms<256, 256, 32, 4, 2, 2, EPI, 3>(g); return true;
+    case 28: launch_ms<256, 256, 64, 2, 2, 4, EPI, 3>(g); return true;       // 8 waves, continuous ring
+    case 29: launch_ms<192, 256, 64, 2, 2, 4, EPI, 3>(g); return true;
+    case 30: launch_ms<256, 256, 64, 2, 2, 4, EPI, 1, 1, 2>(g); return true;  // diag: cached loads
+    case 31: launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 2>(g); return true;
+    case 32: launch_ms<192, 256, 64, 2, 2, 2, EPI, 3>(g); return true;
+    case 33: launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 0, 16>(g); return true;  // 16x16x32
+    case 34: launch_ms<192, 256, 64, 2, 2, 2, EPI, 3, 1, 0, 16>(g); return true;
+    case 35: launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 2, 16>(g); return true;  // diag
     case 7: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 1>(g); return true;    // diag: compute only
     case 8: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 2>(g); return true;    // diag: loads only
     default: return false;
@@ -833,6 +941,14 @@ static bool run_table(int cfg, GemmArgs &g) {
 // path; a 192-row tile is taken when it quantises the grid onto the 256 CUs
 // better (M = 8704: 34 -> 46 row tiles), and 128x128 tiles for grids too
 // small to fill the chip twice with 256x256 tiles.
+static int g_family = 0;   // hd_gemm_set_family
+
+extern "C" int hd_gemm_set_family(int family) {
+    const int prev = g_family;
+    g_family = family == 1 ? 1 : 0;
+    return prev;
+}
+
 static double quant_eff(long tiles) {
     long rounds = (tiles + 255) / 256;
     return (double)tiles / (double)(rounds * 256);
@@ -850,9 +966,20 @@ static const char *pick_and_launch(GemmArgs &g, bool launch) {
     }
     // 192-row tiles compute 25% fewer rows per tile for the same overheads;
     // take them only when the quantisation gain outweighs that (~12%).
+    // K <= 8192: 4 waves of 128x128 with one fragment ring across the K loop;
+    // the deep-K (down projection) shapes run faster on 8 interleaved waves.
+    const bool ring = g_family == 0 && g.K <= 8192;
     if (quant_eff(t192) > quant_eff(t256) * 1.12) {
+        if (ring) {
+            if (launch) launch_ms<192, 256, 64, 2, 2, 2, EPI, 3>(g);
+            return "bf16_192x256x64_w2x2_ring";
+        }
         if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 1>(g);
         return "bf16_192x256x64_w2x4_ilv";
+    }
+    if (ring) {
+        if (launch) launch_ms<256, 256, 64, 2, 2, 2, EPI, 3>(g);
+        return "bf16_256x256x64_w2x2_ring";
     }
     if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 1>(g);
     return "bf16_256x256x64_w2x4_ilv";
@@ -871,7 +998,7 @@ static void gemm_launch(int epi, GemmArgs &g) {
     }
 }
 
-// Diagnostics: runs tuning-table configuration `cfg` (0..8) for
+// Diagnostics: runs tuning-table configuration `cfg` (0..35) for
 // epilogue 0 (plain) or 3 (SwiGLU, w1 = up). Returns 0 when launched.
 extern "C" int hd_gemm_tune_run(int cfg, int epi, const void *x, const void *w0, const void *w1,
                                 void *y, int M, int N, int K) {
