@@ -160,13 +160,17 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
 
         // tile max on raw scores (the positive scale commutes with max)
         const int kv0 = t * FA_BK;
+        // masking is decided per tile and wave: keys past S, causal rows
+        // whose diagonal falls in the tile, or a dense mask
+        const bool need_mask = MASKED && (a.mask != nullptr || kv0 + FA_BK > a.S ||
+                                          (q0 < a.ar_len && kv0 + FA_BK - 1 > q0));
         float mt = -INFINITY;
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 float v = s[j][r];
-                if (MASKED) {
+                if (need_mask) {
                     const int kv = kv0 + j * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
                     bool dead = kv >= a.S || (my_q < a.ar_len && kv > my_q);
                     if (a.mask && !dead && my_q < a.S)

@@ -258,3 +258,20 @@ def test_sched_and_patchify_bit_exact(pkg, lib, dev):
     back = torch.empty_like(imgd)
     lib.hd_unpatchify_f32(pkg.ptr(tok), pkg.ptr(back), 3, 2, 3, 32)
     assert torch.equal(back, imgd)
+
+
+@pytest.mark.parametrize("Hq,Hkv,S,ar", [(4, 2, 40, 0), (4, 2, 64, 0), (4, 2, 100, 0), (4, 2, 128, 0),
+                                         (8, 2, 333, 120), (8, 2, 1024, 0), (8, 2, 1024, 700)])
+def test_flash_tile_edges(pkg, lib, dev, Hq, Hkv, S, ar):
+    # one and two K/V tiles, ragged tails, causal prefixes ending inside and
+    # past the first query tiles
+    D = 128
+    q, k, v = _attn_inputs(Hq, Hkv, S, D, 3 * S + Hq)
+    plan = pkg.SdpaPlan(1, Hq, Hkv, S, D, ar_len=ar)
+    qd, kd, vd = dbf(q, dev), dbf(k, dev), dbf(v, dev)
+    out = torch.zeros(Hq, S, D, dtype=torch.bfloat16, device=dev)
+    rc = lib.hd_sdpa_execute(plan.h, pkg.ptr(qd), pkg.ptr(kd), pkg.ptr(vd), None, pkg.ptr(out), None)
+    assert rc == 0, lib.hd_cuda_last_error()
+    ref = orc.attention(q, k, v, None, ar, round_=0)
+    got = host(out).transpose(1, 0, 2).reshape(S, Hq * D)
+    assert rel_l2(got, ref) < 8e-3 and cosine(got, ref) > 0.99995
