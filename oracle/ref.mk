@@ -4,12 +4,14 @@
 #   src/runtime/torch_rng.c  - torch CPU MT19937 randn
 #   src/model/scheduler.c    - sigma derivations (its device-step wrappers
 #                              stay unresolved and are never called)
+#   src/runtime/decode.c     - latent -> RGB uint8 decode
 REF ?= /root/reference
 OUT := _ref
 CC ?= gcc
 CFLAGS = -O2 -fPIC -std=gnu11 -w -I$(REF)/include -I$(REF)/src/cuda -I$(REF)/src/model -I$(REF)/src/runtime
 
-$(OUT)/libref.so: $(REF)/src/runtime/torch_rng.c $(REF)/src/model/scheduler.c
+$(OUT)/libref.so: $(REF)/src/runtime/torch_rng.c $(REF)/src/model/scheduler.c \
+                  $(REF)/src/runtime/decode.c
 	@mkdir -p $(OUT)
 	$(CC) $(CFLAGS) -shared -o $@ $^ -lm
 

@@ -174,3 +174,24 @@ def test_decode_to_rgb_matches_oracle(pkg, lib):
     out = np.empty((2 * 4, 3 * 4, 3), np.uint8)
     lib.hd_decode_to_rgb(pkg.np_ptr(z), 2, 3, 4, 3, pkg.np_ptr(out))
     assert np.array_equal(out, orc.decode_to_rgb(z, 2, 3, 4, 3))
+
+
+def test_decode_to_rgb_matches_reference_build(pkg, lib, ref):
+    # decode.c compiled from the reference sources: random latents beyond
+    # [-1, 1] plus every half-step between output codes (rounding ties)
+    rng = np.random.default_rng(5)
+    gh, gw, p, C = 3, 5, 8, 3
+    n = gh * gw * C * p * p
+    z = (rng.standard_normal(n) * 1.2).astype(np.float32)
+    ties = (2.0 * (np.arange(255) + 0.5) / 255.0 - 1.0).astype(np.float32)
+    z[:255] = ties
+    z[255:510] = np.nextafter(ties, np.float32(2.0))
+    z[510:515] = [-1.0, 1.0, -1.5, 1.5, 0.0]
+    got = np.empty((gh * p, gw * p, C), np.uint8)
+    want = np.empty_like(got)
+    lib.hd_decode_to_rgb(pkg.np_ptr(z), gh, gw, p, C, pkg.np_ptr(got))
+    ref.hd_decode_to_rgb.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int, ctypes.c_void_p]
+    ref.hd_decode_to_rgb.restype = None
+    ref.hd_decode_to_rgb(z.ctypes.data, gh, gw, p, C, want.ctypes.data)
+    assert np.array_equal(got, want)
