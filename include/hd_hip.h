@@ -131,6 +131,26 @@ void hd_sched_flow_match_step(const void *z_dev, const float *mo_dev,
 void hd_sched_cfg_guided(const float *mo_cond, const float *mo_uncond, float g,
                          float *mo_guided, int n);
 
+/* ---- FlowUniPC pointwise kernels (hd_cuda.h:183-198), fp32 -------------
+ * convert: conv = sample - sigma_cur * mo
+ * correct: x = (sig_t/sig_s0) last - alpha_t h_phi_1 mo0;
+ *          corr = rhos_c1 (conv - mo0)                       (order 1)
+ *               = rhos_c0 (mo_old - mo0) inv_rks0 + rhos_c1 (conv - mo0)   (2)
+ *          out = x - alpha_t B_h corr
+ * predict: x = (sig_t/sig_s0) sample - alpha_t h_phi_1 mo0;
+ *          order 2: x -= alpha_t B_h (rhos_p (mo_old - mo0) inv_rks0)
+ * The products a*b - c*d are evaluated as fma(a, b, -(c*d)) and x - a*b as
+ * fma(-a, b, x); sig_t/sig_s0, alpha_t*h_phi_1 and alpha_t*B_h are fp32. */
+void hd_unipc_convert(const float *sample_dev, const float *mo_dev, float sigma_cur,
+                      float *conv_dev, int n);
+void hd_unipc_correct(const float *last_dev, const float *mo0_dev, const float *mo_old_dev,
+                      const float *conv_dev, float sig_t, float sig_s0, float alpha_t,
+                      float h_phi_1, float B_h, float rhos_c0, float rhos_c1, float inv_rks0,
+                      int order_c, float *out_dev, int n);
+void hd_unipc_predict(const float *sample_dev, const float *mo0_dev, const float *mo_old_dev,
+                      float sig_t, float sig_s0, float alpha_t, float h_phi_1, float B_h,
+                      float rhos_p, float inv_rks0, int order_p, float *out_dev, int n);
+
 /* ---- fused kernels (extension) ----------------------------------------
  * The block composes these instead of the one-op-per-launch reference
  * chain; each reproduces the reference's bf16 rounding points exactly. */

@@ -8,7 +8,8 @@
  *
  * Replaces (same names, same struct layouts, same results):
  *   src/runtime/torch_rng.h:30-56     hd_torch_rng_*  / hd_torch_randn_f32
- *   src/model/scheduler.h             hd_scheduler_* (sigma derivations, Euler step)
+ *   src/model/scheduler.h             hd_scheduler_* (sigma derivations, Euler step,
+ *                                     UniPC plan and CPU step)
  *   src/runtime/sequence.c:102-142    T2I position ids and causal-prefix mask
  *   src/runtime/generate.c:78-104     initial noise (seed + 1) and pixel_unshuffle
  */
@@ -69,6 +70,48 @@ hd_status hd_scheduler_step(hd_scheduler *s, const void *z_bf16, const float *mo
                             const float *noise_post_clamp, float s_noise, void *z_next_bf16,
                             int n, float *scratch);
 
+/* ---- FlowUniPC multistep, solver order 2, bh2, predict_x0 (scheduler.h:107-178)
+ * Same struct layouts as the reference. The per-step coefficients are derived
+ * on the host in fp64 (hd_scheduler_unipc_plan); the pointwise math runs on
+ * the device (hd_unipc_convert / hd_unipc_correct / hd_unipc_predict). */
+#define HD_UNIPC_ORDER 2
+typedef struct {
+    float *model_outputs[HD_UNIPC_ORDER]; /* ring, newest at index ORDER-1 */
+    float *last_sample;                   /* pre-predictor sample */
+    int has_last_sample;
+    int this_order;
+    int lower_order_nums;
+    int step_index;
+} hd_scheduler_unipc;
+
+typedef struct {
+    int corr_order;        /* corrector order (0: no corrector) */
+    int pred_order;        /* predictor order (1 during warm-up, 2 after) */
+    int next_this_order;   /* persist for the next step's corrector */
+    int next_lower_order;  /* persist: warm-up counter */
+    double c_sig_t, c_sig_s0, c_alpha_t;
+    double c_h_phi_1, c_B_h;
+    double c_rhos0, c_rhos1, c_inv_rks0;
+    double p_sig_t, p_sig_s0, p_alpha_t;
+    double p_h_phi_1, p_B_h;
+    double p_rhos_p, p_inv_rks0;
+} hd_unipc_plan;
+
+/* scheduler.h:170: coefficients for step si given the persisted predictor
+ * order (this_order, 0 on the first step) and warm-up counter. */
+void hd_scheduler_unipc_plan(const hd_scheduler *s, int si, int this_order,
+                             int lower_order_nums, hd_unipc_plan *plan);
+/* scheduler.h:174: one whole UniPC step on host arrays (convert, optional
+ * corrector, history shift, predictor), fp64 scalar math; scratch: n floats. */
+hd_status hd_scheduler_unipc_step(const hd_scheduler *s, hd_scheduler_unipc *u,
+                                  const float *model_output, const float *sample,
+                                  float *prev_sample, int n, float *scratch);
+
+/* Per-step SDE noise of the flash/dev samplers (generate.c:907-925): n draws
+ * of hd_torch_randn_f32, then, when clip > 0, clamped to +-clip * std (std
+ * unbiased, fp64 accumulation). */
+void hd_step_noise(hd_torch_rng *rng, float *out, int64_t n, float clip);
+
 /* ---- sequence tables (sequence.c:102-142) ------------------------------ */
 /* T2I position ids, pos [3, S] fp32, S = text_len + grid_h*grid_w: text row i
  * = (i, i, i); image token (r, c) = fix_point + (0, r, c). */
@@ -92,11 +135,14 @@ void hd_pixel_unshuffle(const float *img, int channels, int height, int width, i
 void hd_decode_to_rgb(const float *z_f32, int grid_h, int grid_w, int patch, int channels,
                       unsigned char *out);
 
-/* ---- denoising loop (extension; generate.c:1314-1455 restated) ---------
- * Flow-match Euler with classifier-free guidance, batch 2 in one forward
- * (row 0 = cond ids, row 1 = uncond ids), all on the device:
- *   for i in [0, steps):  t = sigma_i for both rows
- *     x = hd_forward_batched(ids, z, t)               [2, S, 3072]
+/* ---- denoising loops (extension; generate.c:855-935 and :1314-1455) ----
+ * The model is fed t = 1 - sigma_i, and sigma_i is floored at 1e-6 before the
+ * velocity division, as the reference's step loops do.
+ *
+ * hd_denoise_euler_cfg: flow-match Euler with classifier-free guidance, batch
+ * 2 in one forward (row 0 = cond ids, row 1 = uncond ids), all on the device:
+ *   for i in [0, steps):
+ *     x = hd_forward_batched(ids, z, 1 - sigma_i)     [2, S, 3072]
  *     mo_c = (z - x_c[img])/sigma_i, mo_u likewise    (hd_sched_vcond)
  *     mo = (1-g) mo_u + g mo_c                        (hd_sched_cfg_guided)
  *     z = bf16(z + (sigma_{i+1} - sigma_i) mo)        (hd_sched_flow_match_step)
@@ -110,6 +156,28 @@ hd_status hd_denoise_euler_cfg(const hd_forward_binding *bw, hd_forward_workspac
                                int steps, float guidance, int seq, int heads, int kv_heads,
                                int hidden, int ff_hidden, int head_dim, int tms_token_id,
                                void *scratch, int64_t scratch_bytes, void *stream);
+
+/* hd_denoise: the reference's three samplers on the device.
+ *   HD_SAMPLER_EULER  flow_match: z = bf16(z + (s_{i+1} - s_i) mo)
+ *   HD_SAMPLER_FLASH  dev/flash SDE: per-step noise (hd_step_noise from
+ *                     seed + 1, clip noise_clip_std), s_noise ramped from
+ *                     s_noise_start to s_noise_end, hd_scheduler_step
+ *   HD_SAMPLER_UNIPC  default: FlowUniPC order 2 (hd_scheduler_unipc_plan +
+ *                     hd_unipc_*), z = bf16(predictor output)
+ * batch 2 runs classifier-free guidance (row 0 cond, row 1 uncond, combined
+ * with `guidance`); batch 1 runs the conditional forward only. The sigma
+ * schedule comes from `sched` (steps + 1 values). Scratch:
+ * hd_denoise_run_scratch_bytes(). The flash sampler's noise is drawn on the
+ * host into pinned staging while the previous step's forward runs. */
+enum { HD_SAMPLER_EULER = 0, HD_SAMPLER_FLASH = 1, HD_SAMPLER_UNIPC = 2 };
+int64_t hd_denoise_run_scratch_bytes(int batch, int seq, int img_tokens, int steps);
+hd_status hd_denoise(const hd_forward_binding *bw, hd_forward_workspace *ws, int sampler,
+                     const hd_scheduler *sched, int steps, int batch, const int64_t *ids_dev,
+                     int text_len, const float *pos_dev, int ar_len, void *z_dev, int img_tokens,
+                     float guidance, uint64_t seed, float s_noise_start, float s_noise_end,
+                     float noise_clip_std, int seq, int heads, int kv_heads, int hidden,
+                     int ff_hidden, int head_dim, int tms_token_id, void *scratch,
+                     int64_t scratch_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -635,6 +635,61 @@ extern "C" void hd_sched_cfg_guided(const float *c, const float *u, float g, flo
     hd_check_launch("sched_cfg_guided");
 }
 
+// FlowUniPC pointwise steps (sched.cu:160-263). The per-step scalars
+// r = sig_t/sig_s0, ah = alpha_t*h_phi_1 and ab = alpha_t*B_h are formed once
+// in fp32 on the host (correctly rounded, as the per-element device
+// expressions would be); a*b - c*d is fma(a, b, -(c*d)), x - a*b is fma(-a, b, x).
+__global__ void unipc_convert_kernel(const float *smp, const float *mo, float sigma, float *conv,
+                                     int n) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) conv[i] = fmaf(-sigma, mo[i], smp[i]);
+}
+__global__ void unipc_correct_kernel(const float *last, const float *mo0, const float *mo_old,
+                                     const float *conv, float r, float ah, float ab, float rc0,
+                                     float rc1, float inv_rk, int order, float *out, int n) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float m0 = mo0[i];
+    const float x = fmaf(r, last[i], -(ah * m0));
+    const float d1t = conv[i] - m0;
+    const float corr = order == 2 ? fmaf(rc0, (mo_old[i] - m0) * inv_rk, rc1 * d1t) : rc1 * d1t;
+    out[i] = fmaf(-ab, corr, x);
+}
+__global__ void unipc_predict_kernel(const float *smp, const float *mo0, const float *mo_old,
+                                     float r, float ah, float ab, float rp, float inv_rk, int order,
+                                     float *out, int n) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float m0 = mo0[i];
+    float x = fmaf(r, smp[i], -(ah * m0));
+    if (order == 2) x = fmaf(-ab, rp * ((mo_old[i] - m0) * inv_rk), x);
+    out[i] = x;
+}
+extern "C" void hd_unipc_convert(const float *smp, const float *mo, float sigma, float *conv, int n) {
+    if (!smp || !mo || !conv || n <= 0) BAD("unipc_convert");
+    unipc_convert_kernel<<<hd_cdiv(n, 256), 256, 0, hd_stream()>>>(smp, mo, sigma, conv, n);
+    hd_check_launch("unipc_convert");
+}
+extern "C" void hd_unipc_correct(const float *last, const float *mo0, const float *mo_old,
+                                 const float *conv, float sig_t, float sig_s0, float alpha_t,
+                                 float h_phi_1, float B_h, float rc0, float rc1, float inv_rk,
+                                 int order, float *out, int n) {
+    if (!last || !mo0 || !conv || !out || n <= 0 || (order == 2 && !mo_old)) BAD("unipc_correct");
+    unipc_correct_kernel<<<hd_cdiv(n, 256), 256, 0, hd_stream()>>>(
+        last, mo0, mo_old, conv, sig_t / sig_s0, alpha_t * h_phi_1, alpha_t * B_h, rc0, rc1, inv_rk,
+        order, out, n);
+    hd_check_launch("unipc_correct");
+}
+extern "C" void hd_unipc_predict(const float *smp, const float *mo0, const float *mo_old,
+                                 float sig_t, float sig_s0, float alpha_t, float h_phi_1,
+                                 float B_h, float rp, float inv_rk, int order, float *out, int n) {
+    if (!smp || !mo0 || !out || n <= 0 || (order == 2 && !mo_old)) BAD("unipc_predict");
+    unipc_predict_kernel<<<hd_cdiv(n, 256), 256, 0, hd_stream()>>>(
+        smp, mo0, mo_old, sig_t / sig_s0, alpha_t * h_phi_1, alpha_t * B_h, rp, inv_rk, order, out,
+        n);
+    hd_check_launch("unipc_predict");
+}
+
 // ---------------------------------------------------------------------------
 // Patch (un)shuffle (generate.c:85-104, decode.c:10-27 index rule).
 // Enumerates the token-major layout so the token side is coalesced.

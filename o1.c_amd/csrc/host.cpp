@@ -1,6 +1,6 @@
 // Host modules around the forward: torch CPU MT19937 noise, sigma schedules,
-// sequence tables, initial latent, RGB decode, and the device-side
-// flow-match Euler + CFG denoising loop.
+// the UniPC plan and CPU step, sequence tables, initial latent, RGB decode,
+// and the device-side denoising loops.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdio.h>
@@ -217,6 +217,192 @@ extern "C" hd_status hd_scheduler_step(hd_scheduler *s, const void *z, const flo
 }
 
 // ---------------------------------------------------------------------------
+// FlowUniPC (UniPC, Zhao et al. 2023; bh2 variant, data prediction, order 2)
+// in the flow parametrisation alpha = 1 - sigma, lambda = log(alpha/sigma).
+// The arithmetic order follows scheduler.c:215-330 so the fp64 scalars agree
+// bit for bit; everything here runs on the host.
+// ---------------------------------------------------------------------------
+static double unipc_lambda(double sigma) { return log(1.0 - sigma) - log(sigma); }
+
+// rho for the order-2 corrector: solve [[1, 1], [rk, 1]] x = [b0, b1]
+// (scheduler.c:16-23, :264-274); the singular case keeps rho = (0, 0.5)
+static void unipc_rhos_c(double hh, double phi, double B, double rk, double *r0, double *r1) {
+    double k1 = phi / hh - 1.0;
+    const double b0 = k1 * 1.0 / B;
+    k1 = k1 / hh - 1.0 / 2.0;
+    const double b1 = k1 * 2.0 / B;
+    const double det = 1.0 * 1.0 - 1.0 * rk;
+    if (det == 0.0) {
+        *r0 = 0.0;
+        *r1 = 0.5;
+        return;
+    }
+    *r0 = (b0 * 1.0 - 1.0 * b1) / det;
+    *r1 = (1.0 * b1 - b0 * rk) / det;
+}
+
+extern "C" void hd_scheduler_unipc_plan(const hd_scheduler *s, int si, int this_order,
+                                        int lower_order_nums, hd_unipc_plan *plan) {
+    if (!s || !plan) return;
+    memset(plan, 0, sizeof(*plan));
+    const int n_inf = s->num_steps - 1;
+    if (si < 0 || si >= n_inf) return;
+    if (si > 0 && this_order > 0) {
+        // corrector: refines the sample of step si with the new model output
+        const int co = this_order >= 2 ? 2 : 1;
+        const double st = s->sigmas[si], s0 = s->sigmas[si - 1];
+        const double h = unipc_lambda(st) - unipc_lambda(s0), hh = -h;
+        const double phi = expm1(hh), B = expm1(hh);
+        double rk = 1.0, r0 = 0.0, r1 = 0.5;
+        if (co == 2) {
+            const double sm = si - 2 >= 0 ? (double)s->sigmas[si - 2] : (double)s->sigmas[0];
+            rk = (unipc_lambda(sm) - unipc_lambda(s0)) / h;
+            unipc_rhos_c(hh, phi, B, rk, &r0, &r1);
+        }
+        plan->corr_order = co;
+        plan->c_sig_t = st;
+        plan->c_sig_s0 = s0;
+        plan->c_alpha_t = 1.0 - st;
+        plan->c_h_phi_1 = phi;
+        plan->c_B_h = B;
+        plan->c_rhos0 = r0;
+        plan->c_rhos1 = r1;
+        plan->c_inv_rks0 = rk == 0.0 ? 0.0 : 1.0 / rk;
+    }
+    // predictor: order min(2, steps left) during warm-up limited to
+    // lower_order_nums + 1 (lower_order_final)
+    int po = n_inf - si < 2 ? n_inf - si : 2;
+    if (po > lower_order_nums + 1) po = lower_order_nums + 1;
+    if (po < 1) po = 1;
+    const double st = s->sigmas[si + 1], s0 = s->sigmas[si];
+    const double h = unipc_lambda(st) - unipc_lambda(s0), hh = -h;
+    const double phi = expm1(hh), B = expm1(hh);
+    double rk = 1.0, rp = 0.0;
+    if (po == 2) {
+        const double sm = si - 1 >= 0 ? (double)s->sigmas[si - 1] : (double)s->sigmas[0];
+        rk = (unipc_lambda(sm) - unipc_lambda(s0)) / h;
+        if (rk != 0.0) rp = 0.5;
+    }
+    plan->pred_order = po;
+    plan->p_sig_t = st;
+    plan->p_sig_s0 = s0;
+    plan->p_alpha_t = 1.0 - st;
+    plan->p_h_phi_1 = phi;
+    plan->p_B_h = B;
+    plan->p_rhos_p = rp;
+    plan->p_inv_rks0 = rk == 0.0 ? 0.0 : 1.0 / rk;
+    plan->next_this_order = po;
+    plan->next_lower_order = lower_order_nums < 2 ? lower_order_nums + 1 : lower_order_nums;
+}
+
+extern "C" hd_status hd_scheduler_unipc_step(const hd_scheduler *s, hd_scheduler_unipc *u,
+                                             const float *mo, const float *sample, float *prev,
+                                             int n, float *scratch) {
+    if (!s || !u || !mo || !sample || !prev || !scratch || n <= 0) {
+        hd_set_error("scheduler: unipc: null argument");
+        return HD_ERR_MISSING;
+    }
+    const int si = u->step_index;
+    if (si < 0 || si >= s->num_steps - 1) {
+        hd_set_error("scheduler: unipc: step_index out of range");
+        return HD_ERR_MISSING;
+    }
+    float *m_new = u->model_outputs[HD_UNIPC_ORDER - 1], *m_old = u->model_outputs[0];
+    if (!m_new || !u->last_sample) {
+        hd_set_error("scheduler: unipc: history not initialized");
+        return HD_ERR_MISSING;
+    }
+    // converted model output (data prediction): x0 = sample - sigma * mo
+    float *conv = scratch;
+    const float sc = s->sigmas[si];
+    for (int j = 0; j < n; j++) {
+        const float p = sc * mo[j];
+        conv[j] = sample[j] - p;
+    }
+    for (int j = 0; j < n; j++) prev[j] = sample[j];
+    // The reference's CPU step keeps rk = 1 (its rks[0]) where the per-step
+    // plan uses rk = (lambda_prev - lambda_s0) / h: the order-2 corrector's
+    // 2x2 system is then singular and keeps rho = (0, 0.5), and the order-2
+    // predictor's difference is not divided by rk (scheduler.c:305-380).
+    // hd_denoise follows the plan, as generate.c's production loop does.
+    const double rk_cpu = 1.0;
+    if (si > 0 && u->has_last_sample && u->this_order > 0) {
+        // UniC: the sample of this step from last_sample, using conv_{t-1}
+        // (m_new, before the shift) and conv_{t-2} (m_old)
+        const int order = u->this_order;
+        const double st = s->sigmas[si], s0 = s->sigmas[si - 1];
+        const double h = unipc_lambda(st) - unipc_lambda(s0), hh = -h;
+        const double phi = expm1(hh), B = expm1(hh), at = 1.0 - st;
+        double r0 = 0.0, r1 = 0.5;
+        if (order == 2) unipc_rhos_c(hh, phi, B, rk_cpu, &r0, &r1);
+        const double scale = st / s0, coef = at * phi;
+        for (int j = 0; j < n; j++)
+            prev[j] = (float)(scale * (double)u->last_sample[j] - coef * (double)m_new[j]);
+        if (order == 2) {
+            const double inv = 1.0 / rk_cpu, bc = at * B;
+            for (int j = 0; j < n; j++) {
+                const double d1 = ((double)m_old[j] - (double)m_new[j]) * inv;
+                const double d1t = (double)conv[j] - (double)m_new[j];
+                prev[j] = (float)((double)prev[j] - bc * (r0 * d1 + r1 * d1t));
+            }
+        } else {
+            const double bc = at * B * 0.5;
+            for (int j = 0; j < n; j++)
+                prev[j] = (float)((double)prev[j] - bc * ((double)conv[j] - (double)m_new[j]));
+        }
+    }
+    // history: oldest <- newest <- conv
+    for (int i = 0; i < HD_UNIPC_ORDER - 1; i++)
+        memcpy(u->model_outputs[i], u->model_outputs[i + 1], (size_t)n * sizeof(float));
+    memcpy(m_new, conv, (size_t)n * sizeof(float));
+    int order = s->num_steps - 1 - si < HD_UNIPC_ORDER ? s->num_steps - 1 - si : HD_UNIPC_ORDER;
+    if (order > u->lower_order_nums + 1) order = u->lower_order_nums + 1;
+    u->this_order = order;
+    memcpy(u->last_sample, prev, (size_t)n * sizeof(float));
+    u->has_last_sample = 1;
+    {
+        // UniP from the (corrected) sample in prev, in place
+        const double st = s->sigmas[si + 1], s0 = s->sigmas[si];
+        const double h = unipc_lambda(st) - unipc_lambda(s0), hh = -h;
+        const double phi = expm1(hh), B = expm1(hh), at = 1.0 - st;
+        const float *m0 = u->model_outputs[HD_UNIPC_ORDER - 1];
+        const double scale = st / s0, coef = at * phi;
+        for (int j = 0; j < n; j++)
+            prev[j] = (float)(scale * (double)prev[j] - coef * (double)m0[j]);
+        if (order == 2) {
+            const float *m1 = u->model_outputs[HD_UNIPC_ORDER - 2];
+            const double inv = 1.0 / rk_cpu, bc = at * B * 0.5;
+            for (int j = 0; j < n; j++) {
+                const double d1 = ((double)m1[j] - (double)m0[j]) * inv;
+                prev[j] = (float)((double)prev[j] - bc * d1);
+            }
+        }
+    }
+    if (u->lower_order_nums < HD_UNIPC_ORDER) u->lower_order_nums++;
+    u->step_index++;
+    return HD_OK;
+}
+
+extern "C" void hd_step_noise(hd_torch_rng *rng, float *out, int64_t n, float clip) {
+    if (!rng || !out || n <= 0) return;
+    hd_torch_randn_f32(rng, out, n);
+    if (clip <= 0.0f) return;
+    double mean = 0.0, m2 = 0.0;
+    for (int64_t k = 0; k < n; k++) mean += out[k];
+    mean /= (double)n;
+    for (int64_t k = 0; k < n; k++) {
+        const double d = (double)out[k] - mean;
+        m2 += d * d;
+    }
+    const double sd = sqrt(m2 / (double)(n - 1));
+    const float cv = clip * (float)sd;
+    for (int64_t k = 0; k < n; k++) {
+        if (out[k] > cv) out[k] = cv;
+        else if (out[k] < -cv) out[k] = -cv;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Sequence tables
 // ---------------------------------------------------------------------------
 extern "C" hd_status hd_seq_t2i_positions(int text_len, int gh, int gw, int fix_point, float *pos) {
@@ -306,6 +492,7 @@ extern "C" void hd_decode_to_rgb(const float *z, int gh, int gw, int p, int C, u
 // Flow-match Euler + CFG denoising loop (device resident)
 // ---------------------------------------------------------------------------
 static inline int64_t al256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+static const float kTEps = 1e-6f;   // sigma floor of the velocity division (generate.c:64)
 
 extern "C" int64_t hd_denoise_scratch_bytes(int seq, int img, int steps) {
     const int64_t n = (int64_t)img * 3072;
@@ -343,12 +530,12 @@ extern "C" hd_status hd_denoise_euler_cfg(const hd_forward_binding *bw, hd_forwa
         hd_set_error("denoise: too many steps");
         status = HD_ERR_UNSUPPORTED;
     }
-    // per-step timestep pairs (t = sigma for both rows), written by a fill
-    // kernel: the values travel as kernel arguments, no host buffer outlives
-    // the call
-    for (int i = 0; status == HD_OK && i < steps; i++) hd_fill_f32(tdev + 2 * i, sigmas[i], 2);
+    // per-step timestep pairs (t = 1 - sigma for both rows, generate.c:1315),
+    // written by a fill kernel: the values travel as kernel arguments, no
+    // host buffer outlives the call
+    for (int i = 0; status == HD_OK && i < steps; i++) hd_fill_f32(tdev + 2 * i, 1.0f - sigmas[i], 2);
     for (int i = 0; status == HD_OK && i < steps; i++) {
-        const float sg = sigmas[i], sn = sigmas[i + 1];
+        const float sg = sigmas[i] < kTEps ? kTEps : sigmas[i], sn = sigmas[i + 1];
         for (int b = 0; b < 2 && status == HD_OK; b++)
             if (hipMemcpyAsync(vin + b * n, z, n * 2, hipMemcpyDeviceToDevice, st) != hipSuccess) {
                 hd_set_error("denoise: latent copy failed");
@@ -362,12 +549,182 @@ extern "C" hd_status hd_denoise_euler_cfg(const hd_forward_binding *bw, hd_forwa
         hd_sched_vcond(z, xp + (size_t)T * 3072, sg, mo_c, (int)n);
         hd_sched_vcond(z, xp + ((size_t)S + T) * 3072, sg, mo_u, (int)n);
         hd_sched_cfg_guided(mo_c, mo_u, guidance, mo, (int)n);
-        hd_sched_flow_match_step(z, mo, sg, sn, z, (int)n);
+        hd_sched_flow_match_step(z, mo, sigmas[i], sn, z, (int)n);
         if (hd_cuda_last_error()[0]) {
             hd_set_error("denoise: %s", hd_cuda_last_error());
             status = HD_ERR_RUNTIME;
         }
     }
     hd_hip_set_stream(prev);
+    return status;
+}
+
+// ---------------------------------------------------------------------------
+// hd_denoise: Euler / flash SDE / UniPC samplers, optional CFG (batch 2)
+// ---------------------------------------------------------------------------
+extern "C" int64_t hd_denoise_run_scratch_bytes(int B, int S, int I, int steps) {
+    const int64_t n = (int64_t)I * 3072;
+    return al256((int64_t)B * n * 2)                 // vin [B, I, 3072] bf16
+           + al256((int64_t)B * S * 3072 * 2)        // x_pred [B, S, 3072] bf16
+           + al256(3 * n * 4)                        // mo_c, mo_u, mo
+           + al256(7 * n * 4)                        // sampler state (UniPC: z, 3 conv slots,
+                                                     // last, corrected, predicted; flash: noise
+                                                     // + the step's 3n scratch)
+           + al256((int64_t)(steps + 1) * B * 4);    // timesteps
+}
+
+namespace {
+struct PinnedNoise {
+    float *buf[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    ~PinnedNoise() {
+        for (int k = 0; k < 2; k++) {
+            if (done[k]) {
+                (void)hipEventSynchronize(done[k]);
+                (void)hipEventDestroy(done[k]);
+            }
+            if (buf[k]) (void)hipHostFree(buf[k]);
+        }
+    }
+};
+}  // namespace
+
+extern "C" hd_status hd_denoise(const hd_forward_binding *bw, hd_forward_workspace *ws, int sampler,
+                                const hd_scheduler *sched, int steps, int B, const int64_t *ids,
+                                int T, const float *pos, int ar_len, void *z, int I,
+                                float guidance, uint64_t seed, float sn_start, float sn_end,
+                                float clip, int S, int H, int KV, int HID, int FF, int D, int tms,
+                                void *scratch, int64_t scratch_bytes, void *stream) {
+    if (!bw || !ws || !sched || !ids || !pos || !z || !scratch || I <= 0 || steps < 1) {
+        hd_set_error("denoise: null argument");
+        return HD_ERR_MISSING;
+    }
+    if ((B != 1 && B != 2) || sampler < HD_SAMPLER_EULER || sampler > HD_SAMPLER_UNIPC) {
+        hd_set_error("denoise: batch must be 1 or 2 and sampler 0..2");
+        return HD_ERR_UNSUPPORTED;
+    }
+    if (steps > sched->num_steps - 1) {
+        hd_set_error("denoise: %d steps but the schedule has %d sigmas", steps, sched->num_steps);
+        return HD_ERR_UNSUPPORTED;
+    }
+    if (scratch_bytes < hd_denoise_run_scratch_bytes(B, S, I, steps)) {
+        hd_set_error("denoise: scratch too small");
+        return HD_ERR_OOM;
+    }
+    const int64_t n = (int64_t)I * 3072;
+    char *p = (char *)scratch;
+    uint16_t *vin = (uint16_t *)p; p += al256((int64_t)B * n * 2);
+    uint16_t *xp = (uint16_t *)p; p += al256((int64_t)B * S * 3072 * 2);
+    float *mo_c = (float *)p, *mo_u = mo_c + n, *mo = mo_u + n; p += al256(3 * n * 4);
+    float *st = (float *)p; p += al256(7 * n * 4);
+    float *tdev = (float *)p;
+
+    PinnedNoise pn;
+    hd_torch_rng rng;
+    if (sampler == HD_SAMPLER_FLASH) {
+        for (int k = 0; k < 2; k++)
+            if (hipHostMalloc((void **)&pn.buf[k], n * sizeof(float), hipHostMallocDefault) !=
+                    hipSuccess ||
+                hipEventCreateWithFlags(&pn.done[k], hipEventDisableTiming) != hipSuccess) {
+                hd_set_error("denoise: pinned noise staging failed");
+                return HD_ERR_OOM;
+            }
+        hd_torch_rng_seed(&rng, seed + 1);   // generate.c:1295-1296
+    }
+
+    void *prev_stream = hd_hip_get_stream();
+    if (stream) hd_hip_set_stream(stream);
+    hipStream_t hs = (hipStream_t)hd_hip_get_stream();
+    hd_status status = HD_OK;
+    for (int i = 0; i < steps; i++) hd_fill_f32(tdev + (size_t)B * i, 1.0f - sched->sigmas[i], B);
+
+    // UniPC state: converted outputs rotate through three slots
+    float *zf = st, *slot[3] = {st + n, st + 2 * n, st + 3 * n};
+    float *last = st + 4 * n, *corr_buf = st + 5 * n, *pred = st + 6 * n;
+    int this_order = 0, lower = 0, have_hist = 0;
+    hd_scheduler fs = *sched;   // flash: step_index walks with i
+
+    for (int i = 0; status == HD_OK && i < steps; i++) {
+        const float sig = sched->sigmas[i];
+        const float sg = sig < kTEps ? kTEps : sig;
+        const void *vptr = z;
+        if (B == 2) {
+            for (int b = 0; b < 2 && status == HD_OK; b++)
+                if (hipMemcpyAsync(vin + b * n, z, n * 2, hipMemcpyDeviceToDevice, hs) != hipSuccess) {
+                    hd_set_error("denoise: latent copy failed");
+                    status = HD_ERR_IO;
+                }
+            vptr = vin;
+        }
+        if (status != HD_OK) break;
+        status = hd_forward_batched(bw, ws, B, ids, T, pos, ar_len, vptr, I, tdev + (size_t)B * i,
+                                    S, H, KV, HID, FF, D, tms, nullptr, xp, nullptr);
+        if (status != HD_OK) break;
+        hd_cuda_clear_error();
+        hd_sched_vcond(z, xp + (size_t)T * 3072, sg, mo_c, (int)n);
+        const float *m = mo_c;
+        if (B == 2) {
+            hd_sched_vcond(z, xp + ((size_t)S + T) * 3072, sg, mo_u, (int)n);
+            hd_sched_cfg_guided(mo_c, mo_u, guidance, mo, (int)n);
+            m = mo;
+        }
+        if (sampler == HD_SAMPLER_EULER) {
+            hd_sched_flow_match_step(z, m, sig, sched->sigmas[i + 1], z, (int)n);
+        } else if (sampler == HD_SAMPLER_FLASH) {
+            // the host draws this step's noise while the forward runs; the
+            // staging buffer is reused only after its previous copy is done
+            const int k = i & 1;
+            if (i >= 2) (void)hipEventSynchronize(pn.done[k]);
+            hd_step_noise(&rng, pn.buf[k], n, clip);
+            float *noise_dev = st;
+            if (hipMemcpyAsync(noise_dev, pn.buf[k], n * sizeof(float), hipMemcpyHostToDevice, hs) !=
+                    hipSuccess ||
+                hipEventRecord(pn.done[k], hs) != hipSuccess) {
+                hd_set_error("denoise: noise upload failed");
+                status = HD_ERR_IO;
+                break;
+            }
+            fs.step_index = i;
+            const float s_noise = hd_scheduler_noise_scale(sched, i, sn_start, sn_end);
+            status = hd_scheduler_step(&fs, z, m, noise_dev, s_noise, z, (int)n, st + n);
+        } else {
+            hd_unipc_plan pl;
+            hd_scheduler_unipc_plan(sched, i, this_order, lower, &pl);
+            hd_sched_bf16_upcast(z, zf, (int)n);
+            float *cur = slot[0];
+            hd_unipc_convert(zf, m, sig, cur, (int)n);
+            const float *corr = zf;
+            if (i > 0 && this_order > 0 && have_hist) {
+                hd_unipc_correct(last, slot[1], slot[2], cur, (float)pl.c_sig_t, (float)pl.c_sig_s0,
+                                 (float)pl.c_alpha_t, (float)pl.c_h_phi_1, (float)pl.c_B_h,
+                                 (float)pl.c_rhos0, (float)pl.c_rhos1, (float)pl.c_inv_rks0,
+                                 pl.corr_order, corr_buf, (int)n);
+                corr = corr_buf;
+            }
+            if (hipMemcpyAsync(last, corr, n * sizeof(float), hipMemcpyDeviceToDevice, hs) !=
+                hipSuccess) {
+                hd_set_error("denoise: unipc state copy failed");
+                status = HD_ERR_IO;
+                break;
+            }
+            hd_unipc_predict(corr, cur, slot[1], (float)pl.p_sig_t, (float)pl.p_sig_s0,
+                             (float)pl.p_alpha_t, (float)pl.p_h_phi_1, (float)pl.p_B_h,
+                             (float)pl.p_rhos_p, (float)pl.p_inv_rks0, pl.pred_order, pred, (int)n);
+            hd_f32_convert_bf16(pred, z, (int)n);
+            // conv_t -> slot 1, conv_{t-1} -> slot 2, the oldest buffer is reused
+            float *oldest = slot[2];
+            slot[2] = slot[1];
+            slot[1] = slot[0];
+            slot[0] = oldest;
+            this_order = pl.next_this_order;
+            lower = pl.next_lower_order;
+            have_hist = 1;
+        }
+        if (status == HD_OK && hd_cuda_last_error()[0]) {
+            hd_set_error("denoise: %s", hd_cuda_last_error());
+            status = HD_ERR_RUNTIME;
+        }
+    }
+    hd_hip_set_stream(prev_stream);
     return status;
 }

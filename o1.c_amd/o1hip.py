@@ -75,6 +75,20 @@ class hd_scheduler(ctypes.Structure):
                 ("noise_clip_std", c_float)]
 
 
+class hd_scheduler_unipc(ctypes.Structure):
+    _fields_ = [("model_outputs", c_void_p * 2), ("last_sample", c_void_p),
+                ("has_last_sample", c_int), ("this_order", c_int), ("lower_order_nums", c_int),
+                ("step_index", c_int)]
+
+
+class hd_unipc_plan(ctypes.Structure):
+    _fields_ = [("corr_order", c_int), ("pred_order", c_int), ("next_this_order", c_int),
+                ("next_lower_order", c_int)] + [(n, ctypes.c_double) for n in (
+                    "c_sig_t", "c_sig_s0", "c_alpha_t", "c_h_phi_1", "c_B_h", "c_rhos0", "c_rhos1",
+                    "c_inv_rks0", "p_sig_t", "p_sig_s0", "p_alpha_t", "p_h_phi_1", "p_B_h",
+                    "p_rhos_p", "p_inv_rks0")]
+
+
 class hd_lora_entry(ctypes.Structure):
     _fields_ = [("lora_prefix", ctypes.c_char * 256), ("base_tensor", ctypes.c_char * 256),
                 ("rank", ctypes.c_uint32), ("in_dim", ctypes.c_uint32),
@@ -205,6 +219,19 @@ SIGNATURES = {
     "hd_denoise_euler_cfg": (c_int, [ctypes.POINTER(hd_forward_binding), ctypes.POINTER(hd_forward_workspace),
                                      P, c_int, P, c_int, P, c_int, P, c_int, c_float, c_int, c_int,
                                      c_int, c_int, c_int, c_int, c_int, P, c_int64, P]),
+    "hd_scheduler_unipc_plan": (None, [ctypes.POINTER(hd_scheduler), c_int, c_int, c_int,
+                                       ctypes.POINTER(hd_unipc_plan)]),
+    "hd_scheduler_unipc_step": (c_int, [ctypes.POINTER(hd_scheduler), ctypes.POINTER(hd_scheduler_unipc),
+                                        P, P, P, c_int, P]),
+    "hd_step_noise": (None, [ctypes.POINTER(hd_torch_rng), P, c_int64, c_float]),
+    "hd_denoise_run_scratch_bytes": (c_int64, [c_int, c_int, c_int, c_int]),
+    "hd_denoise": (c_int, [ctypes.POINTER(hd_forward_binding), ctypes.POINTER(hd_forward_workspace), c_int,
+                           ctypes.POINTER(hd_scheduler), c_int, c_int, P, c_int, P, c_int, P, c_int,
+                           c_float, ctypes.c_uint64, c_float, c_float, c_float, c_int, c_int, c_int,
+                           c_int, c_int, c_int, c_int, P, c_int64, P]),
+    "hd_unipc_convert": (None, [P, P, c_float, P, c_int]),
+    "hd_unipc_correct": (None, [P, P, P, P] + [c_float] * 8 + [c_int, P, c_int]),
+    "hd_unipc_predict": (None, [P, P, P] + [c_float] * 7 + [c_int, P, c_int]),
 }
 
 _lib = None

@@ -434,6 +434,46 @@ void o1o_sched_cfg_guided(const float *c, const float *u, float g, float *o, int
     for (int i = 0; i < n; i++) o[i] = fmaf(g, c[i], (1.0f - g) * u[i]);
 }
 
+/* sched.cu:162-170 */
+void o1o_unipc_convert(const float *smp, const float *mo, float sigma, float *conv, int n) {
+    for (int i = 0; i < n; i++) conv[i] = fmaf(-sigma, mo[i], smp[i]);
+}
+/* sched.cu:172-201: x_t = (sig_t/sig_s0) last - alpha_t h_phi_1 m0;
+ * out = x_t - alpha_t B_h corr */
+void o1o_unipc_correct(const float *last, const float *mo0, const float *mo_old, const float *conv,
+                       float sig_t, float sig_s0, float alpha_t, float h_phi_1, float B_h,
+                       float rc0, float rc1, float inv_rk, int order, float *out, int n) {
+    const float r = sig_t / sig_s0, ah = alpha_t * h_phi_1, ab = alpha_t * B_h;
+    for (int i = 0; i < n; i++) {
+        const float m0 = mo0[i];
+        const float x = fmaf(r, last[i], -(ah * m0));
+        const float d1t = conv[i] - m0;
+        float corr;
+        if (order == 2) {
+            const float d1s = (mo_old[i] - m0) * inv_rk;
+            corr = fmaf(rc0, d1s, rc1 * d1t);
+        } else {
+            corr = rc1 * d1t;
+        }
+        out[i] = fmaf(-ab, corr, x);
+    }
+}
+/* sched.cu:203-228 */
+void o1o_unipc_predict(const float *smp, const float *mo0, const float *mo_old, float sig_t,
+                       float sig_s0, float alpha_t, float h_phi_1, float B_h, float rp,
+                       float inv_rk, int order, float *out, int n) {
+    const float r = sig_t / sig_s0, ah = alpha_t * h_phi_1, ab = alpha_t * B_h;
+    for (int i = 0; i < n; i++) {
+        const float m0 = mo0[i];
+        float x = fmaf(r, smp[i], -(ah * m0));
+        if (order == 2) {
+            const float d1s = (mo_old[i] - m0) * inv_rk;
+            x = fmaf(-ab, rp * d1s, x);
+        }
+        out[i] = x;
+    }
+}
+
 /* generate.c:85-104: tok[r*Wp+c][ch*p*p + i*p + j] = img[ch][r*p+i][c*p+j] */
 void o1o_patchify(const float *img, float *tok, int C, int Hp, int Wp, int p) {
     const size_t W = (size_t)Wp * p, Hh = (size_t)Hp * p, F = (size_t)C * p * p;

@@ -104,6 +104,15 @@ void o1o_sched_vcond(const float *z, const float *xp, float sigma, float *mo, in
 void o1o_sched_flow_match_step(const float *z, const float *mo, float sigma, float sigma_next,
                                float *zn, int n);
 void o1o_sched_cfg_guided(const float *c, const float *u, float g, float *o, int n);
+/* sched.cu:160-263 FlowUniPC pointwise steps, with the fma placement the
+ * device kernels state (a*b - c*d = fma(a, b, -(c*d)); x - a*b = fma(-a, b, x)) */
+void o1o_unipc_convert(const float *smp, const float *mo, float sigma, float *conv, int n);
+void o1o_unipc_correct(const float *last, const float *mo0, const float *mo_old, const float *conv,
+                       float sig_t, float sig_s0, float alpha_t, float h_phi_1, float B_h,
+                       float rc0, float rc1, float inv_rk, int order, float *out, int n);
+void o1o_unipc_predict(const float *smp, const float *mo0, const float *mo_old, float sig_t,
+                       float sig_s0, float alpha_t, float h_phi_1, float B_h, float rp,
+                       float inv_rk, int order, float *out, int n);
 
 /* generate.c:85-104 / decode.c:5-27 */
 void o1o_patchify(const float *img, float *tok, int C, int Hp, int Wp, int p);

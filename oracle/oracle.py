@@ -68,6 +68,9 @@ def lib():
         L.o1o_sched_vcond.argtypes = [F, F, c_float, F, c_int]
         L.o1o_sched_flow_match_step.argtypes = [F, F, c_float, c_float, F, c_int]
         L.o1o_sched_cfg_guided.argtypes = [F, F, c_float, F, c_int]
+        L.o1o_unipc_convert.argtypes = [F, F, c_float, F, c_int]
+        L.o1o_unipc_correct.argtypes = [F, F, F, F] + [c_float] * 8 + [c_int, F, c_int]
+        L.o1o_unipc_predict.argtypes = [F, F, F] + [c_float] * 7 + [c_int, F, c_int]
         L.o1o_patchify.argtypes = [F, F, c_int, c_int, c_int, c_int]
         L.o1o_unpatchify.argtypes = [F, F, c_int, c_int, c_int, c_int]
         L.o1o_decode_to_rgb.argtypes = [F, c_int, c_int, c_int, c_int,
@@ -274,6 +277,30 @@ def sched_flow_match_step(z, mo, sigma, sigma_next):
     zn = np.empty_like(z)
     lib().o1o_sched_flow_match_step(fp(z), fp(mo), sigma, sigma_next, fp(zn), z.size)
     return zn
+
+
+def unipc_convert(smp, mo, sigma):
+    smp, mo = f32(smp), f32(mo)
+    o = np.empty_like(smp)
+    lib().o1o_unipc_convert(fp(smp), fp(mo), sigma, fp(o), smp.size)
+    return o
+
+
+def unipc_correct(last, mo0, mo_old, conv, sig_t, sig_s0, alpha_t, h_phi_1, B_h, rc0, rc1, inv_rk,
+                  order):
+    last, mo0, mo_old, conv = f32(last), f32(mo0), f32(mo_old), f32(conv)
+    o = np.empty_like(last)
+    lib().o1o_unipc_correct(fp(last), fp(mo0), fp(mo_old), fp(conv), sig_t, sig_s0, alpha_t, h_phi_1,
+                            B_h, rc0, rc1, inv_rk, order, fp(o), last.size)
+    return o
+
+
+def unipc_predict(smp, mo0, mo_old, sig_t, sig_s0, alpha_t, h_phi_1, B_h, rp, inv_rk, order):
+    smp, mo0, mo_old = f32(smp), f32(mo0), f32(mo_old)
+    o = np.empty_like(smp)
+    lib().o1o_unipc_predict(fp(smp), fp(mo0), fp(mo_old), sig_t, sig_s0, alpha_t, h_phi_1, B_h, rp,
+                            inv_rk, order, fp(o), smp.size)
+    return o
 
 
 def sched_cfg_guided(c, u, g):

@@ -86,9 +86,32 @@ def scheduler_sigmas(path="/root/reference/tests/unit/oracle_dump.txt"):
     return {"source": "tests/unit/oracle_dump.txt (RECIPE/SIGMAS rows)", "recipes": recipes}
 
 
+def scheduler_matrix(path="/root/reference/tests/unit/oracle_dump_matrix.txt"):
+    """Per-recipe sigmas, noise scales and one sampler result from the
+    upstream scheduler dump (the draws are torch MT19937 seed 1234: z, mo,
+    unused, and for flash one more noise, 64 values each, recipe by recipe;
+    mo is scaled by 0.3; flash/flow_match record one step, default (UniPC)
+    three steps with constant mo)."""
+    recipes = []
+    cur = None
+    for line in open(path):
+        parts = line.split()
+        if not parts or parts[0].startswith("#"):
+            continue
+        if parts[0] == "RECIPE":
+            cur = {"name": parts[1], "steps": int(parts[2]), "shift": float(parts[3]),
+                   "kind": parts[4], "explicit_timesteps": parts[5] == "True"}
+            recipes.append(cur)
+        elif parts[0] in ("SIGMAS", "NOISESCALE", "STEP") and cur is not None:
+            cur[parts[0].lower()] = [float(v) for v in parts[1:]]
+    return {"source": "tests/unit/oracle_dump_matrix.txt", "seed": 1234, "n": 64,
+            "recipes": recipes}
+
+
 if __name__ == "__main__":
     for name, fn in (("gemm_smoke.json", gemm_smoke), ("positions_s23.json", positions),
-                     ("bf16_rne.json", bf16_rne), ("scheduler_sigmas.json", scheduler_sigmas)):
+                     ("bf16_rne.json", bf16_rne), ("scheduler_sigmas.json", scheduler_sigmas),
+                     ("scheduler_matrix.json", scheduler_matrix)):
         with open(os.path.join(HERE, name), "w") as f:
             json.dump(fn(), f, indent=1)
         print("wrote", name)

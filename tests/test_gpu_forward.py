@@ -210,7 +210,7 @@ def test_denoise_loop_matches_stepwise(pkg, lib, dev):
     loop(z1, sig[:2])
     out = torch.empty(2, S, 3072, dtype=torch.bfloat16, device=dev)
     vin = z0.unsqueeze(0).repeat(2, 1, 1).contiguous()
-    td = torch.full((2,), sig[0], dtype=torch.float32, device=dev)
+    td = torch.full((2,), float(np.float32(1.0) - np.float32(sig[0])), dtype=torch.float32, device=dev)
     st = lib.hd_forward_batched(ctypes.byref(model.binding), ctypes.byref(ws), 2, pkg.ptr(idsd), T,
                                 pkg.ptr(posd), 0, pkg.ptr(vin), I, pkg.ptr(td), S, H, KV, HID, FF,
                                 D, TMS, None, pkg.ptr(out), None)
@@ -247,3 +247,113 @@ def test_scheduler_step_device(pkg, lib, dev):
     want = ((noise.cpu().double() * sn).float().double() + (1 - sn) * den.double()).float()
     want = want.to(torch.bfloat16).float()
     assert rel_l2(zn.float().cpu(), want) < 3e-3
+
+
+@pytest.mark.parametrize("sampler,batch", [(0, 1), (0, 2), (1, 1), (2, 2), (2, 1)])
+def test_denoise_samplers_match_stepwise(pkg, lib, dev, sampler, batch):
+    """hd_denoise (Euler / flash SDE / UniPC, with and without CFG) equals the
+    same steps composed by hand from the library's own calls, bit for bit:
+    forward at t = 1 - sigma, velocity, CFG, then the sampler (flash: host
+    noise from seed + 1 clipped at 8 std and hd_scheduler_step; UniPC: the
+    per-step plan and the hd_unipc_* kernels with the three-slot history)."""
+    import importlib
+    synth = importlib.import_module("o1c_amd.synthetic")
+    nL, HID, H, KV, FF, D = 1, 512, 4, 2, 1024, 128
+    T, gh, gw = 16, 8, 8
+    I = gh * gw
+    S = T + I
+    n = I * 3072
+    tens = synth.build_model(n_layers=nL, hidden=HID, heads=H, kv_heads=KV, ff=FF, seed=9)
+    model = synth.Model(tens, nL)
+    pkg.set_block_config(theta=1e4)
+    posd = torch.from_numpy(grid_pos(T, gh, gw)).to(dev)
+    g = torch.Generator().manual_seed(5)
+    ids = torch.randint(0, 151643, (batch, T), generator=g)
+    ids[:, -1] = TMS
+    idsd = ids.to(dev)
+    z0 = torch.randn(I, 3072, generator=g).to(dev, torch.bfloat16)
+    sch = pkg.hd_scheduler()
+    steps = 4
+    if sampler == 1:
+        lib.hd_scheduler_derive_flash(ctypes.byref(sch), steps, 3.0, 8.0)
+    else:
+        lib.hd_scheduler_derive_default(ctypes.byref(sch), steps, 3.0, 8.0)
+    sig = [sch.sigmas[i] for i in range(sch.num_steps)]
+    wsb = lib.hd_forward_batched_workspace_bytes(batch, S, I, H, KV, HID, FF, D)
+    buf = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    ws = pkg.hd_forward_workspace()
+    ws.hidden_a = buf.data_ptr()
+    sb = lib.hd_denoise_run_scratch_bytes(batch, S, I, steps)
+    scratch = torch.empty(sb, dtype=torch.uint8, device=dev)
+    seed, guidance = 77, 4.0
+    z = z0.clone()
+    st = lib.hd_denoise(ctypes.byref(model.binding), ctypes.byref(ws), sampler, ctypes.byref(sch), steps,
+                        batch, pkg.ptr(idsd), T, pkg.ptr(posd), 0, pkg.ptr(z), I, guidance, seed, 8.0, 8.0,
+                        8.0, S, H, KV, HID, FF, D, TMS, pkg.ptr(scratch), sb, None)
+    pkg.check_status(st, "denoise")
+    torch.cuda.synchronize()
+    assert float((z.float() - z0.float()).abs().mean()) > 1e-3
+
+    # the same steps by hand
+    zr = z0.clone()
+    out = torch.empty(batch, S, 3072, dtype=torch.bfloat16, device=dev)
+    mo_c = torch.empty(n, dtype=torch.float32, device=dev)
+    mo_u = torch.empty_like(mo_c)
+    mo = torch.empty_like(mo_c)
+    rng = pkg.hd_torch_rng()
+    lib.hd_torch_rng_seed(ctypes.byref(rng), seed + 1)
+    fs = pkg.hd_scheduler()
+    ctypes.memmove(ctypes.byref(fs), ctypes.byref(sch), ctypes.sizeof(sch))
+    zf, corr_b, last, pred = (torch.empty_like(mo_c) for _ in range(4))
+    slots = [torch.empty_like(mo_c) for _ in range(3)]
+    this_order = lower = have = 0
+    sscr = torch.empty(3 * n, dtype=torch.float32, device=dev)
+    for i in range(steps):
+        s_i = np.float32(sig[i])
+        vin = zr.unsqueeze(0).repeat(batch, 1, 1).contiguous()
+        td = torch.full((batch,), float(np.float32(1.0) - s_i), dtype=torch.float32, device=dev)
+        st = lib.hd_forward_batched(ctypes.byref(model.binding), ctypes.byref(ws), batch, pkg.ptr(idsd), T,
+                                    pkg.ptr(posd), 0, pkg.ptr(vin), I, pkg.ptr(td), S, H, KV, HID, FF,
+                                    D, TMS, None, pkg.ptr(out), None)
+        pkg.check_status(st, "forward")
+        sg = max(float(s_i), 1e-6)
+        lib.hd_sched_vcond(pkg.ptr(zr), pkg.ptr(out[0, T:]), sg, pkg.ptr(mo_c), n)
+        m = mo_c
+        if batch == 2:
+            lib.hd_sched_vcond(pkg.ptr(zr), pkg.ptr(out[1, T:]), sg, pkg.ptr(mo_u), n)
+            lib.hd_sched_cfg_guided(pkg.ptr(mo_c), pkg.ptr(mo_u), guidance, pkg.ptr(mo), n)
+            m = mo
+        if sampler == 0:
+            lib.hd_sched_flow_match_step(pkg.ptr(zr), pkg.ptr(m), sig[i], sig[i + 1], pkg.ptr(zr), n)
+        elif sampler == 1:
+            noise = np.empty(n, np.float32)
+            lib.hd_step_noise(ctypes.byref(rng), pkg.np_ptr(noise), n, 8.0)
+            nd = torch.from_numpy(noise).to(dev)
+            fs.step_index = i
+            sn = lib.hd_scheduler_noise_scale(ctypes.byref(sch), i, 8.0, 8.0)
+            st = lib.hd_scheduler_step(ctypes.byref(fs), pkg.ptr(zr), pkg.ptr(m), pkg.ptr(nd), sn,
+                                       pkg.ptr(zr), n, pkg.ptr(sscr))
+            pkg.check_status(st, "scheduler step")
+        else:
+            pl = pkg.hd_unipc_plan()
+            lib.hd_scheduler_unipc_plan(ctypes.byref(sch), i, this_order, lower, ctypes.byref(pl))
+            lib.hd_sched_bf16_upcast(pkg.ptr(zr), pkg.ptr(zf), n)
+            cur = slots[0]
+            lib.hd_unipc_convert(pkg.ptr(zf), pkg.ptr(m), sig[i], pkg.ptr(cur), n)
+            corr = zf
+            if i > 0 and this_order > 0 and have:
+                lib.hd_unipc_correct(pkg.ptr(last), pkg.ptr(slots[1]), pkg.ptr(slots[2]), pkg.ptr(cur),
+                                     pl.c_sig_t, pl.c_sig_s0, pl.c_alpha_t, pl.c_h_phi_1, pl.c_B_h,
+                                     pl.c_rhos0, pl.c_rhos1, pl.c_inv_rks0, pl.corr_order,
+                                     pkg.ptr(corr_b), n)
+                corr = corr_b
+            last.copy_(corr)
+            lib.hd_unipc_predict(pkg.ptr(corr), pkg.ptr(cur), pkg.ptr(slots[1]), pl.p_sig_t, pl.p_sig_s0,
+                                 pl.p_alpha_t, pl.p_h_phi_1, pl.p_B_h, pl.p_rhos_p, pl.p_inv_rks0,
+                                 pl.pred_order, pkg.ptr(pred), n)
+            lib.hd_f32_convert_bf16(pkg.ptr(pred), pkg.ptr(zr), n)
+            slots = [slots[2], slots[0], slots[1]]
+            this_order, lower, have = pl.next_this_order, pl.next_lower_order, 1
+        pkg.check_prim("step %d" % i)
+    torch.cuda.synchronize()
+    assert torch.equal(z, zr)

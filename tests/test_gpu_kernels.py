@@ -275,3 +275,28 @@ def test_flash_tile_edges(pkg, lib, dev, Hq, Hkv, S, ar):
     ref = orc.attention(q, k, v, None, ar, round_=0)
     got = host(out).transpose(1, 0, 2).reshape(S, Hq * D)
     assert rel_l2(got, ref) < 8e-3 and cosine(got, ref) > 0.99995
+
+
+@pytest.mark.parametrize("order", [1, 2])
+def test_unipc_kernels_match_oracle(pkg, lib, dev, order):
+    # hd_unipc_* against the C restatement, bit for bit, including the last
+    # step (sig_t = 0, where lambda is infinite and the plan's h_phi_1 = -1)
+    n = 4099
+    rng = np.random.default_rng(order)
+    a, b, c, d = (rng.standard_normal(n).astype(np.float32) for _ in range(4))
+    da, db, dc, dd = (torch.from_numpy(v).to(dev) for v in (a, b, c, d))
+    out = torch.empty(n, dtype=torch.float32, device=dev)
+    lib.hd_unipc_convert(pkg.ptr(da), pkg.ptr(db), 0.73, pkg.ptr(out), n)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(out), orc.unipc_convert(a, b, 0.73))
+    for sig_t, sig_s0 in ((0.61, 0.7), (0.0, 0.1)):
+        at = 1.0 - sig_t
+        phi = -0.3 if sig_t else -1.0
+        args = (sig_t, sig_s0, at, phi, phi * 1.01, 0.37, 0.52, 1.0 / -0.9)
+        lib.hd_unipc_correct(pkg.ptr(da), pkg.ptr(db), pkg.ptr(dc), pkg.ptr(dd), *args, order, pkg.ptr(out), n)
+        torch.cuda.synchronize()
+        assert np.array_equal(host(out), orc.unipc_correct(a, b, c, d, *args, order))
+        pargs = (sig_t, sig_s0, at, phi, phi * 1.01, 0.5, 1.0 / -0.9)
+        lib.hd_unipc_predict(pkg.ptr(da), pkg.ptr(db), pkg.ptr(dc), *pargs, order, pkg.ptr(out), n)
+        torch.cuda.synchronize()
+        assert np.array_equal(host(out), orc.unipc_predict(a, b, c, *pargs, order))

@@ -195,3 +195,160 @@ def test_decode_to_rgb_matches_reference_build(pkg, lib, ref):
     ref.hd_decode_to_rgb.restype = None
     ref.hd_decode_to_rgb(z.ctypes.data, gh, gw, p, C, want.ctypes.data)
     assert np.array_equal(got, want)
+
+
+def _sched_from(pkg, sigmas):
+    s = pkg.hd_scheduler()
+    for i, v in enumerate(sigmas):
+        s.sigmas[i] = v
+    s.num_steps = len(sigmas)
+    return s
+
+
+def _ref_unipc_types(ref, pkg):
+    P = ctypes.c_void_p
+    ref.hd_scheduler_unipc_plan.argtypes = [ctypes.POINTER(pkg.hd_scheduler), ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_int, ctypes.POINTER(pkg.hd_unipc_plan)]
+    ref.hd_scheduler_unipc_plan.restype = None
+    ref.hd_scheduler_unipc_step.argtypes = [ctypes.POINTER(pkg.hd_scheduler),
+                                            ctypes.POINTER(pkg.hd_scheduler_unipc), P, P, P, ctypes.c_int, P]
+    ref.hd_scheduler_unipc_step.restype = ctypes.c_int
+
+
+def _plan_tuple(pl):
+    return tuple(getattr(pl, n) for n, _ in pl._fields_)
+
+
+@pytest.mark.parametrize("recipe", ["default50", "flash28", "short3"])
+def test_unipc_plan_matches_reference_build(pkg, lib, ref, recipe):
+    # the reference's scheduler.c (oracle/_ref) on the same sigma arrays:
+    # every field of every step's plan, bit for bit
+    _ref_unipc_types(ref, pkg)
+    s = pkg.hd_scheduler()
+    if recipe == "default50":
+        lib.hd_scheduler_derive_default(ctypes.byref(s), 50, 3.0, 0.0)
+    elif recipe == "flash28":
+        lib.hd_scheduler_derive_flash(ctypes.byref(s), 28, 3.0, 0.0)
+    else:
+        lib.hd_scheduler_derive_default(ctypes.byref(s), 3, 1.0, 0.0)
+    this_order, lower = 0, 0
+    for si in range(s.num_steps - 1):
+        for to, lo in ((this_order, lower), (2, 2), (1, 0)):
+            a, b = pkg.hd_unipc_plan(), pkg.hd_unipc_plan()
+            lib.hd_scheduler_unipc_plan(ctypes.byref(s), si, to, lo, ctypes.byref(a))
+            ref.hd_scheduler_unipc_plan(ctypes.byref(s), si, to, lo, ctypes.byref(b))
+            ta, tb = _plan_tuple(a), _plan_tuple(b)
+            assert all((x == y) or (x != x and y != y) for x, y in zip(ta, tb)), (si, to, lo, ta, tb)
+        # follow the persisted orders of the production loop
+        st = pkg.hd_unipc_plan()
+        lib.hd_scheduler_unipc_plan(ctypes.byref(s), si, this_order, lower, ctypes.byref(st))
+        this_order, lower = st.next_this_order, st.next_lower_order
+
+
+def _unipc_state(pkg, n):
+    bufs = [np.zeros(n, np.float32) for _ in range(3)]
+    u = pkg.hd_scheduler_unipc()
+    u.model_outputs[0] = bufs[0].ctypes.data
+    u.model_outputs[1] = bufs[1].ctypes.data
+    u.last_sample = bufs[2].ctypes.data
+    return u, bufs
+
+
+def test_unipc_step_matches_reference_build(pkg, lib, ref):
+    # whole CPU steps (convert, corrector, history, predictor) against
+    # scheduler.c, with a fresh model output every step, bit for bit
+    _ref_unipc_types(ref, pkg)
+    s = pkg.hd_scheduler()
+    lib.hd_scheduler_derive_default(ctypes.byref(s), 8, 3.0, 0.0)
+    n = 257
+    rng = np.random.default_rng(11)
+    ua, keep_a = _unipc_state(pkg, n)
+    ub, keep_b = _unipc_state(pkg, n)
+    xa = rng.standard_normal(n).astype(np.float32)
+    xb = xa.copy()
+    scr_a, scr_b = np.empty(n, np.float32), np.empty(n, np.float32)
+    for i in range(8):
+        mo = (rng.standard_normal(n) * 0.5).astype(np.float32)
+        pa, pb = np.empty(n, np.float32), np.empty(n, np.float32)
+        assert lib.hd_scheduler_unipc_step(ctypes.byref(s), ctypes.byref(ua), pkg.np_ptr(mo), pkg.np_ptr(xa),
+                                           pkg.np_ptr(pa), n, pkg.np_ptr(scr_a)) == 0
+        assert ref.hd_scheduler_unipc_step(ctypes.byref(s), ctypes.byref(ub), mo.ctypes.data, xb.ctypes.data,
+                                           pb.ctypes.data, n, scr_b.ctypes.data) == 0
+        assert np.array_equal(pa, pb), i
+        assert (ua.this_order, ua.lower_order_nums, ua.step_index) == \
+               (ub.this_order, ub.lower_order_nums, ub.step_index)
+        xa, xb = pa, pb
+
+
+def test_scheduler_matrix_golden(pkg, lib):
+    # tests/unit/oracle_dump_matrix.txt (upstream torch schedulers): the
+    # draws replayed from MT19937 seed 1234, then one flash SDE step (noise
+    # clip 8 std, s_noise 8), one flow-match Euler step, and three UniPC
+    # steps with constant mo, at the reference test's tolerances
+    g = json.load(open(os.path.join(ROOT, "tests", "golden", "scheduler_matrix.json")))
+    n = g["n"]
+    rng = pkg.hd_torch_rng()
+    lib.hd_torch_rng_seed(ctypes.byref(rng), g["seed"])
+
+    def draw():
+        v = np.empty(n, np.float32)
+        lib.hd_torch_randn_f32(ctypes.byref(rng), pkg.np_ptr(v), n)
+        return v
+
+    for r in g["recipes"]:
+        s = pkg.hd_scheduler()
+        if r["explicit_timesteps"]:
+            lib.hd_scheduler_derive_dev(ctypes.byref(s), 8.0)
+        elif r["kind"] == "flash":
+            lib.hd_scheduler_derive_flash(ctypes.byref(s), r["steps"], r["shift"], 8.0)
+        elif r["kind"] == "flow_match":
+            lib.hd_scheduler_derive_flow_match(ctypes.byref(s), r["steps"], r["shift"], 8.0)
+        else:
+            lib.hd_scheduler_derive_default(ctypes.byref(s), r["steps"], r["shift"], 8.0)
+        sig = np.array(s.sigmas[:s.num_steps], np.float32)
+        assert np.abs(sig - np.array(r["sigmas"], np.float32)).max() <= 1e-6, r["name"]
+        z, mo, _ = draw(), draw(), draw()
+        mo = (mo * np.float32(0.3)).astype(np.float32)
+        want = np.array(r["step"], np.float32)
+        s0, s1 = np.float32(sig[0]), np.float32(sig[1])
+        if r["kind"] == "flash":
+            noise = np.empty(n, np.float32)
+            lib.hd_step_noise(ctypes.byref(rng), pkg.np_ptr(noise), n, 8.0)
+            den = (z - mo * s0).astype(np.float32)
+            got = ((s1 * noise) * np.float32(8.0) + (np.float32(1.0) - s1) * den).astype(np.float32)
+            assert np.abs(got - want).max() <= 1e-5, r["name"]
+        elif r["kind"] == "flow_match":
+            got = (z + (s1 - s0) * mo).astype(np.float32)
+            assert np.abs(got - want).max() <= 1e-5, r["name"]
+        else:
+            u, keep = _unipc_state(pkg, n)
+            smp = z.copy()
+            scr = np.empty(n, np.float32)
+            for _ in range(3):
+                out = np.empty(n, np.float32)
+                assert lib.hd_scheduler_unipc_step(ctypes.byref(s), ctypes.byref(u), pkg.np_ptr(mo),
+                                                   pkg.np_ptr(smp), pkg.np_ptr(out), n, pkg.np_ptr(scr)) == 0
+                smp = out
+            assert np.abs(smp - want).max() <= 1e-4, r["name"]
+            # the per-step plan with the device kernels' arithmetic (oracle
+            # restatement): the production path, within 1e-6 of upstream
+            from oracle import oracle as orc
+            smp, hist, last, to, lo = z.copy(), [None, None], None, 0, 0
+            for i in range(3):
+                pl = pkg.hd_unipc_plan()
+                lib.hd_scheduler_unipc_plan(ctypes.byref(s), i, to, lo, ctypes.byref(pl))
+                cur = orc.unipc_convert(smp, mo, s.sigmas[i])
+                corr = smp
+                if pl.corr_order:
+                    old = hist[1] if hist[1] is not None else hist[0]
+                    corr = orc.unipc_correct(last, hist[0], old, cur, pl.c_sig_t, pl.c_sig_s0,
+                                             pl.c_alpha_t, pl.c_h_phi_1, pl.c_B_h, pl.c_rhos0,
+                                             pl.c_rhos1, pl.c_inv_rks0, pl.corr_order)
+                last = corr.copy()
+                prev_conv = hist[0] if hist[0] is not None else cur
+                smp = orc.unipc_predict(corr, cur, prev_conv, pl.p_sig_t, pl.p_sig_s0, pl.p_alpha_t,
+                                        pl.p_h_phi_1, pl.p_B_h, pl.p_rhos_p, pl.p_inv_rks0,
+                                        pl.pred_order)
+                hist = [cur, hist[0]]
+                to, lo = pl.next_this_order, pl.next_lower_order
+            assert np.abs(smp - want).max() <= 1e-6, r["name"]
