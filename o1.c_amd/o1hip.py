@@ -39,9 +39,26 @@ class hd_device_alloc(ctypes.Structure):
 
 
 class hd_weight_store(ctypes.Structure):
-    _fields_ = [("device_id", c_int), ("allocs", ctypes.POINTER(hd_device_alloc)),
-                ("n_allocs", c_int64), ("arena_ptr", c_void_p), ("arena_bytes", c_int64),
-                ("upload_stream", c_void_p)]
+    _fields_ = [("device_id", c_int), ("device_name", ctypes.c_char * 256), ("compute_major", c_int),
+                ("compute_minor", c_int), ("device_mem_bytes", c_int64), ("host_bytes_loaded", c_int64),
+                ("device_bytes_allocated", c_int64), ("n_allocations", c_int64),
+                ("largest_numel", c_int64), ("largest_name", ctypes.c_char * 256),
+                ("allocs", ctypes.POINTER(hd_device_alloc)), ("n_allocs", c_int64), ("gemm", c_void_p),
+                ("arena_ptr", c_void_p), ("arena_bytes", c_int64), ("upload_stream", c_void_p)]
+
+
+class hd_gguf_tensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("n_dims", ctypes.c_uint32), ("dims", ctypes.c_uint64 * 8),
+                ("type", ctypes.c_uint32), ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64)]
+
+
+class hd_gguf_file(ctypes.Structure):
+    _fields_ = [("path", ctypes.c_char_p), ("n_tensors", c_int64),
+                ("tensors", ctypes.POINTER(hd_gguf_tensor)), ("alignment", ctypes.c_uint64),
+                ("tensor_data_off", ctypes.c_uint64), ("payload_bytes", ctypes.c_uint64)] + [
+                (n, ctypes.c_char_p) for n in ("arch", "name", "profile", "variant", "revision", "dtype",
+                                               "quantization")] + [
+                ("num_layers", c_int64), ("layout_version", c_int64)]
 
 
 class hd_forward_binding(ctypes.Structure):
@@ -169,6 +186,14 @@ SIGNATURES = {
     "hd_flash_make_vt": (None, [P, P, c_int, c_int]),
     # hd_weights.h
     "hd_weight_store_find": (P, [ctypes.POINTER(hd_weight_store), c_char_p]),
+    "hd_device_info": (c_int, [c_int, ctypes.POINTER(hd_weight_store)]),
+    "hd_weights_to_device_gguf": (c_int, [c_char_p, c_int, ctypes.POINTER(hd_weight_store)]),
+    "hd_weight_store_free": (None, [ctypes.POINTER(hd_weight_store)]),
+    "hd_weights_last_error": (c_char_p, []),
+    "hd_gguf_open": (c_int, [c_char_p, ctypes.POINTER(hd_gguf_file)]),
+    "hd_gguf_close": (None, [ctypes.POINTER(hd_gguf_file)]),
+    "hd_gguf_read_tensor": (c_int, [ctypes.POINTER(hd_gguf_file), ctypes.POINTER(hd_gguf_tensor), P]),
+    "hd_gguf_last_error": (c_char_p, []),
     # hd_block.h
     "hd_block_get_config": (None, [ctypes.POINTER(hd_block_config)]),
     "hd_block_set_config": (None, [ctypes.POINTER(hd_block_config)]),

@@ -31,3 +31,19 @@ def dev():
     import __graft_entry__ as ge
     ge.load_package().bind_torch_stream()
     return torch.device("cuda:0")
+
+
+@pytest.fixture(autouse=True)
+def _restore_block_config(request):
+    """Tests that change the process-wide block config (rotary theta, eps,
+    section) must not leak it into later tests."""
+    if "lib" not in request.fixturenames and "dev" not in request.fixturenames:
+        yield
+        return
+    import ctypes
+    pk = request.getfixturevalue("pkg")
+    lb = request.getfixturevalue("lib")
+    saved = pk.hd_block_config()
+    lb.hd_block_get_config(ctypes.byref(saved))
+    yield
+    lb.hd_block_set_config(ctypes.byref(saved))
