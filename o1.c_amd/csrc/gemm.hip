@@ -269,6 +269,22 @@ template <int N> __device__ __forceinline__ void wait_vm_barrier() {
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
+// 16-byte buffer load straight to LDS (buffer_load_dwordx4 ... lds): base and
+// nbytes form the scalar descriptor (reads at or past nbytes return zero).
+// The descriptor type exists in the device pass only.
+__device__ __forceinline__ void buf_load_lds16(const void *base, int nbytes, uint32_t voff, uint32_t soff,
+                                               HD_LDS void *dst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    // the descriptor must live in SGPRs: base and size are wave-uniform
+    const uint64_t b = (uint64_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(((uint64_t)hi << 32) | lo), 0, __builtin_amdgcn_readfirstlane(nbytes), 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, soff, 0, 0);
+#endif
+}
+
 // as above, and the wave's own LDS reads have completed (the barrier then
 // also means no wave still reads the stage about to be refilled)
 template <int N> __device__ __forceinline__ void wait_lgk_vm_barrier() {
@@ -359,8 +375,57 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
     // LDR 2 (diagnostic): every K tile re-reads tile 0, so all loads hit in
     // cache and the instruction stream is otherwise unchanged
     auto koff = [&](int kt) { return LDR == 2 ? 0 : kt * BK; };
+    // LDR 5: buffer loads straight to LDS (MUBUF: 32-bit per-lane byte
+    // offsets against a scalar descriptor; the K advance is the scalar
+    // offset; rows past the matrix read as zero through the record limit)
+    // segment of this column tile (QKV) / the gate and up matrices (SwiGLU)
+    const int bt0 = tn * BN;
+    const int bsg = EPI == EPI_SWIGLU ? 0 : (bt0 < g.seg_end[0] ? 0 : (bt0 < g.seg_end[1] ? 1 : 2));
+    const int bbase = bsg == 0 ? 0 : (bsg == 1 ? g.seg_end[0] : g.seg_end[1]);
+    const int brows = EPI == EPI_SWIGLU ? g.N
+                                        : (bsg == 0 ? g.seg_end[0] : (bsg == 1 ? g.seg_end[1] : g.seg_end[2])) - bbase;
+    const void *bp_a = g.A, *bp_b0 = bsg == 0 ? g.B[0] : (bsg == 1 ? g.B[1] : g.B[2]), *bp_b1 = g.B[1];
+    const int nb_a = (int)((size_t)g.M * g.K * 2), nb_b = (int)((size_t)brows * g.K * 2);
+    uint32_t a_vo[AI], b_vo[BI];
+    int b_rs[BI];
+    if constexpr (LDR == 5) {
+#pragma unroll
+        for (int i = 0; i < AI; i++) {
+            const int r = (wave * AI + i) * C::RPI + sub;
+            a_vo[i] = ((uint32_t)(m0 + r) * (uint32_t)g.K + (uint32_t)(cl ^ ms_swz<CPR>(r)) * 8) * 2;
+        }
+#pragma unroll
+        for (int i = 0; i < BI; i++) {
+            const int r = (wave * BI + i) * C::RPI + sub;
+            int n;
+            if (EPI == EPI_SWIGLU) {
+                const int grp = r / WTN, j = r % WTN;
+                n = tn * C::BN_OUT + grp * (WTN / 2) + (j % (WTN / 2));
+                // the RPI rows of one load share a side of the gate/up split:
+                // decide it from the wave-uniform first row
+                b_rs[i] = (((wave * BI + i) * C::RPI) % WTN) < WTN / 2 ? 0 : 1;
+            } else {
+                n = bt0 + r - bbase;
+                b_rs[i] = 0;
+            }
+            b_vo[i] = n >= brows ? 0x80000000u   // past the records (< 2^31): reads zero
+                                 : ((uint32_t)n * (uint32_t)g.K + (uint32_t)(cl ^ ms_swz<CPR>(r)) * 8) * 2;
+        }
+    }
     auto issue = [&](int kt, int st) {
+        if (LDR == 3) return;   // diagnostic: no global->LDS traffic
         uint16_t *As = smem + st * C::STAGE, *Bs = As + BM * BK;
+        if constexpr (LDR == 5) {
+            const uint32_t so = (uint32_t)kt * BK * 2;
+#pragma unroll
+            for (int i = 0; i < AI; i++)
+                buf_load_lds16(bp_a, nb_a, a_vo[i], so, (HD_LDS void *)(As + (wave * AI + i) * 512));
+#pragma unroll
+            for (int i = 0; i < BI; i++)
+                buf_load_lds16(b_rs[i] ? bp_b1 : bp_b0, nb_b, b_vo[i], so,
+                               (HD_LDS void *)(Bs + (wave * BI + i) * 512));
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < AI; i++)
             __builtin_amdgcn_global_load_lds((const void *)(a_src[i] + koff(kt)),
@@ -412,6 +477,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
         const int lr = lane % MF, lc = lane / MF, swr = ms_swz<CPR>(lr);
         bf16x8_t af[2][TM], bw[2][TN];
         auto ld = [&](const uint16_t *As, int ks, int sl) {
+            if (LDR == 4 && ks + 1 > 0 && sl >= 0 && As != smem) return;   // diagnostic: no fragment reads
             const uint16_t *Bs = As + BM * BK;
             const int c = ((ks * CPS + lc) ^ swr) * 8;
 #pragma unroll
@@ -931,6 +997,15 @@ static bool run_table(int cfg, GemmArgs &g) {
     case 33: launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 0, 16>(g); return true;  // 16x16x32
     case 34: launch_ms<192, 256, 64, 2, 2, 2, EPI, 3, 1, 0, 16>(g); return true;
     case 35: launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 2, 16>(g); return true;  // diag
+    case 36: launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 3>(g); return true;  // diag: no loads
+    case 37: launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 4>(g); return true;  // diag: no frag reads
+    case 38: launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 5>(g); return true;  // buffer loads
+    case 39: launch_ms<192, 256, 64, 2, 2, 2, EPI, 3, 1, 5>(g); return true;
+    case 40: launch_ms<256, 256, 64, 2, 2, 4, EPI, 1, 1, 5>(g); return true;
+    case 41: launch_ms<192, 256, 64, 2, 2, 4, EPI, 1, 1, 5>(g); return true;
+    case 42: launch_ms<256, 256, 32, 4, 2, 2, EPI, 3, 1, 5>(g); return true;
+    case 43: launch_ms<192, 256, 32, 4, 2, 2, EPI, 3, 1, 5>(g); return true;
+    case 44: launch_ms<256, 256, 32, 3, 2, 2, EPI, 3, 1, 5>(g); return true;
     case 7: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 1>(g); return true;    // diag: compute only
     case 8: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 2>(g); return true;    // diag: loads only
     default: return false;
@@ -966,20 +1041,24 @@ static const char *pick_and_launch(GemmArgs &g, bool launch) {
     }
     // 192-row tiles compute 25% fewer rows per tile for the same overheads;
     // take them only when the quantisation gain outweighs that (~12%).
-    // K <= 8192: 4 waves of 128x128 with one fragment ring across the K loop;
-    // the deep-K (down projection) shapes run faster on 8 interleaved waves.
-    const bool ring = g_family == 0 && g.K <= 8192;
+    // K <= 8192: 4 waves of 128x128 with one fragment ring across the K loop,
+    // operands through buffer loads straight to LDS (byte offsets must stay
+    // below 2^31: each operand under 2 GiB); the deep-K (down projection)
+    // shapes run faster on 8 interleaved waves.
+    const bool fits = (size_t)(g.M + 256) * g.K * 2 < ((size_t)1 << 31) &&
+                      (size_t)g.N * g.K * 2 < ((size_t)1 << 31);
+    const bool ring = g_family == 0 && g.K <= 8192 && fits;
     if (quant_eff(t192) > quant_eff(t256) * 1.12) {
         if (ring) {
-            if (launch) launch_ms<192, 256, 64, 2, 2, 2, EPI, 3>(g);
-            return "bf16_192x256x64_w2x2_ring";
+            if (launch) launch_ms<192, 256, 64, 2, 2, 2, EPI, 3, 1, 5>(g);
+            return "bf16_192x256x64_w2x2_ring_buf";
         }
         if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 1>(g);
         return "bf16_192x256x64_w2x4_ilv";
     }
     if (ring) {
-        if (launch) launch_ms<256, 256, 64, 2, 2, 2, EPI, 3>(g);
-        return "bf16_256x256x64_w2x2_ring";
+        if (launch) launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 5>(g);
+        return "bf16_256x256x64_w2x2_ring_buf";
     }
     if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 1>(g);
     return "bf16_256x256x64_w2x4_ilv";
