@@ -14,7 +14,7 @@
 //    h*4..h*4+3 and 8+h*4..8+h*4+3) is matched by storing V^T with bits 2
 //    and 3 of the key index swapped ("vt" layout below), so every operand
 //    fetch is one 16-byte LDS read;
-//  * K and V^T tiles go global -> LDS with global_load_lds_dwordx4 into two
+//  * K and V^T tiles go global -> LDS with buffer_load_dwordx4 ... lds into two
 //    buffers (64 keys per tile), XOR-swizzled by row.
 //
 // vt layout: [B, Hkv, 128, S_pad] bf16, S_pad = round_up(S, 64), key s
@@ -51,6 +51,20 @@ struct FaArgs {
     float inv_scale;       // 1 / scale (mask values are added to raw scores)
     int out_seq_major;
 };
+
+// 16-byte buffer load straight to LDS against a wave-uniform descriptor
+// (base, nbytes); the descriptor type exists in the device pass only
+__device__ __forceinline__ void fa_buf_load16(const void *base, int nbytes, uint32_t voff, uint32_t soff,
+                                              HD_LDS void *dst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint64_t b = (uint64_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(((uint64_t)hi << 32) | lo), 0, __builtin_amdgcn_readfirstlane(nbytes), 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, soff, 0, 0);
+#endif
+}
 
 __device__ __forceinline__ void fa_wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
@@ -106,24 +120,29 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
     // K tile: 64 rows x 16 chunks; wave instr i covers rows 4*(wave*4+i) ..+4
     // V^T tile: 128 rows x 8 chunks; wave instr i covers rows 8*(wave*4+i) ..+8
     uint16_t *Ks0 = smem, *Vs0 = smem + 2 * FA_BK * FA_D;
+    // buffer loads straight to LDS: per-lane byte offsets fixed for the
+    // block, the tile advance goes in the scalar offset; K rows past S read
+    // as zero (their scores are masked: S % 64 != 0 selects the masked
+    // kernel), V^T columns are zero-padded to S_pad
+    const int kbytes = a.S * FA_D * 2, vbytes = FA_D * a.S_pad * 2;
+    uint32_t k_vo[4], v_vo[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int krow = (wave * 4 + i) * 4 + (lane >> 4);
+        k_vo[i] = (uint32_t)(krow * FA_D + (((lane & 15) ^ (krow & 15)) * 8)) * 2;
+        const int vrow = (wave * 4 + i) * 8 + (lane >> 3);
+        v_vo[i] = (uint32_t)(vrow * a.S_pad + (((lane & 7) ^ (vrow & 7)) * 8)) * 2;
+    }
     auto issue = [&](int t, int buf) {
         uint16_t *Ks = Ks0 + buf * FA_BK * FA_D, *Vs = Vs0 + buf * FA_D * FA_BK;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            int row = (wave * 4 + i) * 4 + (lane >> 4);
-            int c = (lane & 15) ^ (row & 15);
-            int kv = min(t * FA_BK + row, a.S - 1);
-            __builtin_amdgcn_global_load_lds((const void *)(kbase + (size_t)kv * FA_D + c * 8),
-                                             (HD_LDS void *)(Ks + (wave * 4 + i) * 512), 16, 0, 0);
-        }
+        for (int i = 0; i < 4; i++)
+            fa_buf_load16(kbase, kbytes, k_vo[i], (uint32_t)t * FA_BK * FA_D * 2,
+                          (HD_LDS void *)(Ks + (wave * 4 + i) * 512));
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            int row = (wave * 4 + i) * 8 + (lane >> 3);
-            int c = (lane & 7) ^ (row & 7);
-            __builtin_amdgcn_global_load_lds(
-                (const void *)(vbase + (size_t)row * a.S_pad + t * FA_BK + c * 8),
-                (HD_LDS void *)(Vs + (wave * 4 + i) * 512), 16, 0, 0);
-        }
+        for (int i = 0; i < 4; i++)
+            fa_buf_load16(vbase, vbytes, v_vo[i], (uint32_t)t * FA_BK * 2,
+                          (HD_LDS void *)(Vs + (wave * 4 + i) * 512));
     };
 
     f32x16_t o[4];
