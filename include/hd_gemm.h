@@ -80,6 +80,18 @@ int hd_gemm_tune_run(int cfg, int epi, const void *x, const void *w0, const void
  * (diagnostics; static string). */
 const char *hd_gemm_config_name(int M, int N, int K, int epilogue);
 
+/* Extension: the block's QKV projection with the per-head q/k RMSNorm and
+ * rotary (hd_qkv_epilogue semantics, bit-identical) fused into the GEMM
+ * epilogue: x [batch*seq, hidden] against wq/wk/wv, writing q [B,H,S,128],
+ * k [B,KV,S,128] and the flash V^T layout vt [B,KV,128,S]. cs: rotary table
+ * [seq, 64] (cos, sin). Returns 0 when launched, 1 (nothing done) when the
+ * shape is outside the fused path: seq % 64 != 0, head counts not even,
+ * hidden > 8192 or not a multiple of 64, operands of 2 GiB or more. */
+int hd_linear_qkv_rope(const void *x, const void *wq, const void *wk, const void *wv,
+                       const void *qn_w, const void *kn_w, const float *cs, void *q, void *k,
+                       void *vt, int batch, int seq, int heads, int kv_heads, int hidden,
+                       float eps);
+
 /* Diagnostics/tuning: kernel family for the production GEMMs. 0 (default):
  * 4-wave fragment-ring tiles for K <= 8192, 8-wave interleaved tiles above;
  * 1: 8-wave interleaved tiles for every shape. Returns the previous value. */

@@ -143,10 +143,16 @@ static hd_status block_core(const void *in, const float *cs, const void *mask, i
         hd_status st = copy_d2d(ints->ln0, s.ln, (size_t)M * HID * 2);
         if (st != HD_OK) return st;
     }
-    hd_linear_concat3(s.ln, bw->q_proj, H * D, bw->k_proj, KV * D, bw->v_proj, KV * D, s.qkv, M,
-                      HID);
-    hd_qkv_epilogue(s.qkv, bw->q_norm, bw->k_norm, cs, s.q, s.k, nullptr, s.vt, batch, (int)seq,
-                    H, KV, D, eps);
+    // QKV GEMM with q/k norm + rotary + V^T layout in its epilogue; shapes
+    // outside that path take the GEMM then the standalone epilogue kernels
+    if (D != 128 || hd_linear_qkv_rope(s.ln, bw->q_proj, bw->k_proj, bw->v_proj, bw->q_norm,
+                                       bw->k_norm, cs, s.q, s.k, s.vt, batch, (int)seq, H, KV,
+                                       HID, eps) != 0) {
+        hd_linear_concat3(s.ln, bw->q_proj, H * D, bw->k_proj, KV * D, bw->v_proj, KV * D, s.qkv,
+                          M, HID);
+        hd_qkv_epilogue(s.qkv, bw->q_norm, bw->k_norm, cs, s.q, s.k, nullptr, s.vt, batch,
+                        (int)seq, H, KV, D, eps);
+    }
     if (hd_flash_attention(s.q, s.k, s.vt, mask, s.attn, batch, H, KV, (int)seq, D, ar_len, scale,
                            1) != 0)
         return launch_status("attention");

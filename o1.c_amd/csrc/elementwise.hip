@@ -377,7 +377,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const int ncol = (heads + 2 * kv_heads) * D;
     const uint16_t *src = qkv + (size_t)m * ncol + (size_t)hslot * D;
     float x0 = bf2f(src[lane]), x1 = bf2f(src[lane + 64]);
-    float ss = wave_sum(x0 * x0 + x1 * x1);
+    float ss = wave_sum(fmaf(x0, x0, x1 * x1));
     float inv = 1.0f / sqrtf(ss / (float)D + eps);
     const uint16_t *w = hslot < heads ? qn_w : kn_w;
     float y0 = bfround(bf2f(w[lane]) * x0 * inv);

@@ -26,7 +26,7 @@
 #include "../../include/hd_hip.h"
 #include "../../include/hd_gemm.h"
 
-enum { EPI_NONE = 0, EPI_BIAS = 1, EPI_RES = 2, EPI_SWIGLU = 3 };
+enum { EPI_NONE = 0, EPI_BIAS = 1, EPI_RES = 2, EPI_SWIGLU = 3, EPI_QKV = 4 };
 
 struct GemmArgs {
     const uint16_t *A;       // [M, K]
@@ -38,6 +38,13 @@ struct GemmArgs {
     int M, N, K;             // N = output columns
     int ldc;
     int ntm, ntn;            // tile grid
+    // EPI_QKV: per-head q/k RMSNorm + rotary into head-major q, k and the
+    // flash V^T layout (columns: q heads, k heads, v heads of 128)
+    const uint16_t *qn_w, *kn_w;   // [128] norm gains
+    const float2 *cs;              // [seq, 64] (cos, sin)
+    uint16_t *q_out, *k_out, *vt_out;
+    int seq, heads, kv_heads;
+    float eps;
 };
 
 __device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
@@ -316,6 +323,115 @@ struct MsCfg {
 // bank groups (64 banks x 4 bytes)
 template <int CPR> __device__ __forceinline__ int ms_swz(int r) {
     return CPR == 8 ? ((r >> 1) & 7) : ((r >> 2) & 3);
+}
+
+// EPI_QKV epilogue for one wave: its WTM rows x 128 columns (one head) are
+// staged in LDS as the bf16 projection output (the reference's rounding
+// point). q/k heads: lane-per-row RMSNorm (the sum of squares uses the
+// pairing and butterfly order of the standalone kernel, x_l^2 + x_{l+64}^2
+// then xor 32..1, so results are bit-identical) and rotate-half rotary with
+// bf16 rounding of every product, then coalesced stores to [B,H,S,128].
+// v heads: transposed stores into [B,KV,128,S] with key bits 2 and 3
+// exchanged (the flash kernel's V^T layout; S % 64 == 0 so no padding).
+template <int WTM, int LDW>
+__device__ __forceinline__ void qkv_epilogue(const GemmArgs &g, uint16_t *stg, int gm0, int hslot,
+                                             int lane) {
+    const int H = g.heads, KV = g.kv_heads, S = g.seq;
+    if (hslot < H + KV) {
+        const uint16_t *w = hslot < H ? g.qn_w : g.kn_w;
+        for (int r = lane; r < WTM; r += 64) {
+            const int m = gm0 + r;
+            if (m >= g.M) break;
+            uint16_t *row = stg + r * LDW;
+            float v[64];
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const u32x4_t lo = *(const u32x4_t *)(row + c * 8);
+                const u32x4_t hi = *(const u32x4_t *)(row + 64 + c * 8);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float a0 = lo_bf(lo[e]), a1 = hi_bf(lo[e]);
+                    const float b0 = lo_bf(hi[e]), b1 = hi_bf(hi[e]);
+                    v[c * 8 + 2 * e] = fmaf(a0, a0, b0 * b0);
+                    v[c * 8 + 2 * e + 1] = fmaf(a1, a1, b1 * b1);
+                }
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+                for (int k = 0; k < o; k++) v[k] = v[k] + v[k + o];
+            const float inv = 1.0f / sqrtf(v[0] / 128.0f + g.eps);
+            const int s = m % S;
+            const float2 *cs = g.cs + (size_t)s * 64;
+#pragma unroll 4
+            for (int c = 0; c < 8; c++) {
+                const u32x4_t lo = *(const u32x4_t *)(row + c * 8);
+                const u32x4_t hi = *(const u32x4_t *)(row + 64 + c * 8);
+                u32x4_t olo, ohi;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float o0[2], o1[2];
+#pragma unroll
+                    for (int t = 0; t < 2; t++) {
+                        const int l = c * 8 + 2 * e + t;
+                        const float x0 = t ? hi_bf(lo[e]) : lo_bf(lo[e]);
+                        const float x1 = t ? hi_bf(hi[e]) : lo_bf(hi[e]);
+                        const float y0 = bfround(bf2f(w[l]) * x0 * inv);
+                        const float y1 = bfround(bf2f(w[l + 64]) * x1 * inv);
+                        const float2 r2 = cs[l];
+                        o0[t] = bfround(y0 * r2.x) - bfround(y1 * r2.y);
+                        o1[t] = bfround(y1 * r2.x) + bfround(y0 * r2.y);
+                    }
+                    olo[e] = pack_bf2(o0[0], o0[1]);
+                    ohi[e] = pack_bf2(o1[0], o1[1]);
+                }
+                *(u32x4_t *)(row + c * 8) = olo;
+                *(u32x4_t *)(row + 64 + c * 8) = ohi;
+            }
+        }
+        // rows were rewritten by their own lanes; the store pass reads
+        // other lanes' rows of this wave's staging area
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int hx = hslot < H ? hslot : hslot - H, nh = hslot < H ? H : KV;
+        uint16_t *base = hslot < H ? g.q_out : g.k_out;
+#pragma unroll 4
+        for (int r0 = 0; r0 < WTM; r0 += 4) {
+            const int r = r0 + lane / 16, cc = (lane % 16) * 8;
+            const int m = gm0 + r;
+            if (m < g.M) {
+                const int b = m / S, s = m % S;
+                *(u32x4_t *)(base + (((size_t)b * nh + hx) * S + s) * 128 + cc) =
+                    *(const u32x4_t *)(stg + r * LDW + cc);
+            }
+        }
+    } else {
+        const int hk = hslot - H - KV;
+        // lane: d = d0 + lane / 16, 8 storage columns (half of a 16-key group)
+        for (int d0 = 0; d0 < 128; d0 += 4) {
+            const int d = d0 + lane / 16, c = lane % 16;
+#pragma unroll
+            for (int gq = 0; gq < WTM / 128 + (WTM % 128 ? 1 : 0); gq++) {
+                const int grp = gq * 8 + c / 2, half = c % 2;   // 16-key group within the wave
+                if (grp * 16 >= WTM) continue;
+                const int m = gm0 + grp * 16;
+                if (m >= g.M) continue;
+                const int b = m / S, s = m % S;
+                uint16_t vals[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int p = half * 8 + e;                                   // storage column in the group
+                    const int src = (p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1);  // key at that column
+                    vals[e] = stg[(grp * 16 + src) * LDW + d];
+                }
+                u32x4_t pk;
+#pragma unroll
+                for (int e = 0; e < 4; e++) pk[e] = (uint32_t)vals[2 * e] | ((uint32_t)vals[2 * e + 1] << 16);
+                *(u32x4_t *)(g.vt_out + (((size_t)b * KV + hk) * 128 + d) * S + s + half * 8) = pk;
+            }
+        }
+    }
 }
 
 template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 0, int OCC = 1,
@@ -659,6 +775,10 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
     constexpr int CPRO = WO / 8, RPIO = 64 / CPRO;
     const int gm0 = m0 + wm * WTM;
     const int gn0 = tn * C::BN_OUT + wn * WO;
+    if constexpr (EPI == EPI_QKV) {
+        qkv_epilogue<WTM, LDW>(g, stg, gm0, gn0 / 128, lane);
+        return;
+    }
 #pragma unroll 4
     for (int r0 = 0; r0 < WTM; r0 += RPIO) {
         const int r = r0 + lane / CPRO, cc = (lane % CPRO) * 8;
@@ -1075,6 +1195,48 @@ static void gemm_launch(int epi, GemmArgs &g) {
     case EPI_RES: pick_and_launch<EPI_RES>(g, true); break;
     case EPI_SWIGLU: pick_and_launch<EPI_SWIGLU>(g, true); break;
     }
+}
+
+// QKV projection with the q/k RMSNorm + rotary and the V^T layout fused into
+// the GEMM epilogue (EPI_QKV). Returns 1 without launching when the shape is
+// outside the fused path (the caller then runs hd_linear_concat3 +
+// hd_qkv_epilogue, which compute the same values).
+extern "C" int hd_linear_qkv_rope(const void *x, const void *wq, const void *wk, const void *wv,
+                                  const void *qn_w, const void *kn_w, const float *cs, void *q,
+                                  void *k, void *vt, int batch, int seq, int heads, int kv_heads,
+                                  int hidden, float eps) {
+    if (!x || !wq || !wk || !wv || !qn_w || !kn_w || !cs || !q || !k || !vt || batch <= 0 ||
+        seq <= 0 || heads <= 0 || kv_heads <= 0 || hidden <= 0)
+        return 1;
+    const int M = batch * seq, N = (heads + 2 * kv_heads) * 128;
+    const bool ok = g_family == 0 && seq % 64 == 0 && (heads * 128) % 256 == 0 &&
+                    (kv_heads * 128) % 256 == 0 && hidden % 64 == 0 && hidden <= 8192 &&
+                    (size_t)(M + 256) * hidden * 2 < ((size_t)1 << 31) &&
+                    (size_t)heads * 128 * hidden * 2 < ((size_t)1 << 31) &&
+                    ((uintptr_t)x % 16 == 0) && ((uintptr_t)vt % 16 == 0);
+    if (!ok) return 1;
+    GemmArgs g = {};
+    g.A = (const uint16_t *)x;
+    g.B[0] = (const uint16_t *)wq;
+    g.B[1] = (const uint16_t *)wk;
+    g.B[2] = (const uint16_t *)wv;
+    g.seg_end[0] = heads * 128;
+    g.seg_end[1] = (heads + kv_heads) * 128;
+    g.seg_end[2] = N;
+    g.M = M; g.N = N; g.K = hidden; g.ldc = N;
+    g.qn_w = (const uint16_t *)qn_w;
+    g.kn_w = (const uint16_t *)kn_w;
+    g.cs = (const float2 *)cs;
+    g.q_out = (uint16_t *)q;
+    g.k_out = (uint16_t *)k;
+    g.vt_out = (uint16_t *)vt;
+    g.seq = seq; g.heads = heads; g.kv_heads = kv_heads; g.eps = eps;
+    const long tn = N / 256;
+    const long t256 = (long)((M + 255) / 256) * tn, t192 = (long)((M + 191) / 192) * tn;
+    if (quant_eff(t192) > quant_eff(t256) * 1.12) launch_ms<192, 256, 64, 2, 2, 2, EPI_QKV, 3, 1, 5>(g);
+    else launch_ms<256, 256, 64, 2, 2, 2, EPI_QKV, 3, 1, 5>(g);
+    hd_check_launch("linear_qkv_rope");
+    return 0;
 }
 
 // Diagnostics: runs tuning-table configuration `cfg` (0..35) for

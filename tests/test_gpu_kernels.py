@@ -300,3 +300,48 @@ def test_unipc_kernels_match_oracle(pkg, lib, dev, order):
         lib.hd_unipc_predict(pkg.ptr(da), pkg.ptr(db), pkg.ptr(dc), *pargs, order, pkg.ptr(out), n)
         torch.cuda.synchronize()
         assert np.array_equal(host(out), orc.unipc_predict(a, b, c, *pargs, order))
+
+
+@pytest.mark.parametrize("B,S,H,KV,HID", [(2, 256, 4, 2, 512), (1, 1152, 32, 8, 4096), (3, 320, 8, 2, 256),
+                                          (2, 4352, 32, 8, 1024)])
+def test_qkv_rope_fused_matches_unfused(pkg, lib, dev, B, S, H, KV, HID):
+    # hd_linear_qkv_rope (norm + rotary + V^T in the GEMM epilogue) against
+    # hd_linear_concat3 + hd_qkv_epilogue: the same values, bit for bit,
+    # including batches whose sequences share a GEMM tile
+    D = 128
+    g = torch.Generator(device=dev).manual_seed(S + H)
+    x = (torch.randn(B * S, HID, generator=g, device=dev)).to(torch.bfloat16)
+    wq = (torch.randn(H * D, HID, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    wk = (torch.randn(KV * D, HID, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    wv = (torch.randn(KV * D, HID, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    qn = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    kn = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    gh, gw = 8, (S - 16) // 8
+    posd = torch.from_numpy(grid_pos(S - gh * gw, gh, gw)).to(dev)
+    cs = pkg.rope_table(posd, S, D, theta=1e4)
+    outs = []
+    for fused in (True, False):
+        q = torch.zeros(B, H, S, D, dtype=torch.bfloat16, device=dev)
+        k = torch.zeros(B, KV, S, D, dtype=torch.bfloat16, device=dev)
+        vt = torch.zeros(B, KV, D, S, dtype=torch.bfloat16, device=dev)
+        if fused:
+            rc = lib.hd_linear_qkv_rope(pkg.ptr(x), pkg.ptr(wq), pkg.ptr(wk), pkg.ptr(wv), pkg.ptr(qn),
+                                        pkg.ptr(kn), pkg.ptr(cs), pkg.ptr(q), pkg.ptr(k), pkg.ptr(vt),
+                                        B, S, H, KV, HID, 1e-6)
+            assert rc == 0
+        else:
+            qkv = torch.empty(B * S, (H + 2 * KV) * D, dtype=torch.bfloat16, device=dev)
+            lib.hd_linear_concat3(pkg.ptr(x), pkg.ptr(wq), H * D, pkg.ptr(wk), KV * D, pkg.ptr(wv), KV * D,
+                                  pkg.ptr(qkv), B * S, HID)
+            lib.hd_qkv_epilogue(pkg.ptr(qkv), pkg.ptr(qn), pkg.ptr(kn), pkg.ptr(cs), pkg.ptr(q), pkg.ptr(k),
+                                None, pkg.ptr(vt), B, S, H, KV, D, 1e-6)
+        pkg.check_prim("qkv fused=%s" % fused)
+        torch.cuda.synchronize()
+        outs.append((q, k, vt))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    assert float(outs[0][0].float().abs().mean()) > 0.1
+    # outside the fused path nothing is launched
+    assert lib.hd_linear_qkv_rope(pkg.ptr(x), pkg.ptr(wq), pkg.ptr(wk), pkg.ptr(wv), pkg.ptr(qn), pkg.ptr(kn),
+                                  pkg.ptr(cs), pkg.ptr(q), pkg.ptr(k), pkg.ptr(vt), B, S - 8, H, KV, HID,
+                                  1e-6) == 1
