@@ -66,6 +66,20 @@ int hd_flash_attention(const void *q, const void *k, const void *vt,
                        float scale, int out_seq_major);
 
 /* Causal prefix length of a plan (0 for a non-split plan or NULL). */
+/* Extension: hd_flash_attention with a workspace for the tail split. When the
+ * (batch x heads x 128-query tiles) units leave a last, partly filled round
+ * of resident blocks, those units run as 2-8 key-range chunks writing fp32
+ * partials (running max, sum, unnormalised O) into ws, and a merge kernel
+ * combines them; full attention only (no mask, ar_len == 0), otherwise and
+ * when ws_bytes < hd_flash_ws_bytes() it behaves as hd_flash_attention.
+ * Results agree with the unsplit kernel to fp32 rounding of the merge. */
+int hd_flash_attention_ws(const void *q, const void *k, const void *vt, const void *mask,
+                          void *out, int batch, int q_heads, int kv_heads, int seq, int head_dim,
+                          int ar_len, float scale, int out_seq_major, void *ws, int64_t ws_bytes);
+/* Workspace bytes for the tail split on the current device (one round of
+ * resident flash blocks x 128 rows x (128 + 2) floats). */
+int64_t hd_flash_ws_bytes(void);
+
 int hd_sdpa_plan_ar_len(const hd_sdpa_plan *plan);
 
 /* Bytes of the flash kernel's V^T layout [B,Hkv,128,round_up(S,64)]. */

@@ -50,6 +50,11 @@ struct FaArgs {
     float scale_log2;      // scale * log2(e)
     float inv_scale;       // 1 / scale (mask values are added to raw scores)
     int out_seq_major;
+    // tail split: blocks [0, n_whole) each run one (b, head, q tile) unit over
+    // all keys; the units from n_whole on run as `split` chunks of the key
+    // tiles each, writing unnormalised partials to `part` (merged afterwards)
+    int n_whole, split;
+    float *part;           // [n_tail * split][FA_BQ][FA_D] O, then [..][FA_BQ] (m, l)
 };
 
 // 16-byte buffer load straight to LDS against a wave-uniform descriptor
@@ -90,7 +95,12 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
     // consecutive linear ids so they run close together in time.
     const int nqt = (a.q_row_end + FA_BQ - 1) / FA_BQ;
     const int group = a.Hq / a.Hkv;
-    int lin = blockIdx.x;
+    int lin = blockIdx.x, chunk = -1, item = 0;
+    if (lin >= a.n_whole) {
+        item = lin - a.n_whole;
+        chunk = item % a.split;
+        lin = a.n_whole + item / a.split;
+    }
     const int g = lin % group; lin /= group;
     const int qt = lin % nqt; lin /= nqt;
     const int hk = lin % a.Hkv;
@@ -106,7 +116,12 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
         int last_row = min(qt * FA_BQ + FA_BQ, a.q_row_end) - 1;
         if (last_row < a.ar_len) kv_end = last_row + 1;
     }
-    const int ntile = (kv_end + FA_BK - 1) / FA_BK;
+    int t_begin = 0, t_end = (kv_end + FA_BK - 1) / FA_BK;
+    if (chunk >= 0) {
+        const int nt = t_end;
+        t_begin = chunk * nt / a.split;
+        t_end = (chunk + 1) * nt / a.split;
+    }
 
     // ---- Q fragments (B operand of S^T), held for the whole loop ---------
     const uint16_t *qrow = a.q + (((size_t)b * a.Hq + hq) * a.S + min(my_q, a.S - 1)) * FA_D;
@@ -152,12 +167,12 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
         for (int r = 0; r < 16; r++) o[i][r] = 0.f;
     float m_run = -1e30f, l_run = 0.f;
 
-    issue(0, 0);
+    issue(t_begin, t_begin & 1);
     fa_wait_vm0();
     __syncthreads();
-    for (int t = 0; t < ntile; t++) {
+    for (int t = t_begin; t < t_end; t++) {
         const int buf = t & 1;
-        if (t + 1 < ntile) issue(t + 1, buf ^ 1);
+        if (t + 1 < t_end) issue(t + 1, buf ^ 1);
         const uint16_t *Ks = Ks0 + buf * FA_BK * FA_D, *Vs = Vs0 + buf * FA_D * FA_BK;
 
         // S^T for 64 keys: two 32-key tiles
@@ -245,6 +260,23 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
 
     // ---- normalise and store ----------------------------------------------
     const float l_tot = xor32_sum(l_run);
+    if (chunk >= 0) {
+        // partial: O relative to this chunk's running max, with (m, l)
+        float *po = a.part + ((size_t)item * FA_BQ + wave * 32 + l32) * FA_D;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+            for (int gq = 0; gq < 4; gq++) {
+                const int d = dt * 32 + gq * 8 + h * 4;
+                *(f32x4_t *)(po + d) = {o[dt][gq * 4], o[dt][gq * 4 + 1], o[dt][gq * 4 + 2],
+                                        o[dt][gq * 4 + 3]};
+            }
+        if (h == 0) {
+            float2 *pml = (float2 *)(a.part + (size_t)(gridDim.x - a.n_whole) * FA_BQ * FA_D);
+            pml[(size_t)item * FA_BQ + wave * 32 + l32] = make_float2(m_run, l_tot);
+        }
+        return;
+    }
     const float inv = 1.0f / l_tot;
     if (my_q >= a.q_row_end) return;
     uint16_t *dst;
@@ -281,6 +313,58 @@ __global__ __launch_bounds__(256) void fa_vt_kernel(const uint16_t *v, uint16_t 
     }
 }
 
+// Merges the tail units' key-chunk partials: O = sum_i w_i O_i / sum_i w_i l_i
+// with w_i = 2^((m_i - max_j m_j) * scale_log2). One thread per (row, d).
+__global__ __launch_bounds__(256) void fa_merge_kernel(FaArgs a, int n_tail) {
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    const int d = idx % FA_D, row = (idx / FA_D) % FA_BQ, tu = idx / (FA_D * FA_BQ);
+    if (tu >= n_tail) return;
+    const int P = a.split, n_items = n_tail * P;
+    const float2 *pml = (const float2 *)(a.part + (size_t)n_items * FA_BQ * FA_D);
+    float m = -INFINITY;
+    for (int i = 0; i < P; i++) m = fmaxf(m, pml[(size_t)(tu * P + i) * FA_BQ + row].x);
+    float L = 0.f, acc = 0.f;
+    for (int i = 0; i < P; i++) {
+        const float2 ml = pml[(size_t)(tu * P + i) * FA_BQ + row];
+        const float w = __builtin_amdgcn_exp2f((ml.x - m) * a.scale_log2);
+        L = fmaf(w, ml.y, L);
+        acc = fmaf(w, a.part[((size_t)(tu * P + i) * FA_BQ + row) * FA_D + d], acc);
+    }
+    const int nqt = (a.q_row_end + FA_BQ - 1) / FA_BQ, group = a.Hq / a.Hkv;
+    int lin = a.n_whole + tu;
+    const int g = lin % group; lin /= group;
+    const int qt = lin % nqt; lin /= nqt;
+    const int hk = lin % a.Hkv, b = lin / a.Hkv, hq = hk * group + g;
+    const int my_q = qt * FA_BQ + row;
+    if (my_q >= a.q_row_end) return;
+    const size_t o = a.out_seq_major ? (((size_t)b * a.S + my_q) * a.Hq + hq) * FA_D + d
+                                     : (((size_t)b * a.Hq + hq) * a.S + my_q) * FA_D + d;
+    a.out[o] = f2bf(acc * (1.0f / L));
+}
+
+// Resident flash blocks on the current device (occupancy x CUs), cached.
+static int fa_slots() {
+    static int dev_cached = -1, slots = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (dev != dev_cached) {
+        int per_cu = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, flash_fwd_kernel<false>, 256, 0) !=
+                hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 0;
+        slots = per_cu * cus;
+        dev_cached = dev;
+    }
+    return slots;
+}
+
+// Workspace for the tail split: at most one round of partial blocks.
+extern "C" int64_t hd_flash_ws_bytes(void) {
+    const int slots = fa_slots();
+    return (int64_t)(slots > 0 ? slots : 1024) * FA_BQ * (FA_D + 2) * 4;
+}
+
 extern "C" int64_t hd_flash_vt_bytes(int batch, int kv_heads, int seq) {
     return (int64_t)batch * kv_heads * FA_D * fa_spad(seq) * 2;
 }
@@ -300,7 +384,7 @@ extern "C" void hd_flash_make_vt(const void *v, void *vt, int bh, int seq) {
 
 static int fa_launch(const void *q, const void *k, const void *vt, const void *mask, void *out,
                      int batch, int hq, int hkv, int seq, int ar_len, int q_row_end, float scale,
-                     int out_seq_major, hipStream_t st) {
+                     int out_seq_major, hipStream_t st, void *ws = nullptr, int64_t ws_bytes = 0) {
     FaArgs a;
     a.q = (const uint16_t *)q;
     a.k = (const uint16_t *)k;
@@ -317,10 +401,34 @@ static int fa_launch(const void *q, const void *k, const void *vt, const void *m
     a.inv_scale = 1.0f / scale;
     a.out_seq_major = out_seq_major;
     const int nqt = (q_row_end + FA_BQ - 1) / FA_BQ;
-    dim3 grid((unsigned)((size_t)batch * hq * nqt));
+    const int units = batch * hq * nqt;
     bool masked = mask || ar_len > 0 || (seq % FA_BK) != 0;
+    // Tail split (full attention only): the units of the last partial round
+    // of resident blocks run as P key chunks each, launched last, so that
+    // round is filled instead of running a few blocks for a whole round.
+    a.n_whole = units;
+    a.split = 1;
+    a.part = (float *)ws;
+    int n_tail = 0;
+    const int slots = ws ? fa_slots() : 0;
+    if (slots > 0 && !mask && ar_len == 0 && units >= slots) {
+        const int rem = units % slots, ntile = (seq + FA_BK - 1) / FA_BK;
+        int P = rem ? slots / rem : 1;
+        if (P > 8) P = 8;
+        if (P > ntile) P = ntile;
+        if (rem && P >= 2 && (int64_t)rem * P * FA_BQ * (FA_D + 2) * 4 <= ws_bytes) {
+            n_tail = rem;
+            a.n_whole = units - rem;
+            a.split = P;
+        }
+    }
+    dim3 grid((unsigned)(a.n_whole + n_tail * a.split));
     if (masked) flash_fwd_kernel<true><<<grid, 256, 0, st>>>(a);
     else flash_fwd_kernel<false><<<grid, 256, 0, st>>>(a);
+    if (n_tail) {
+        dim3 gm((unsigned)hd_cdiv((int64_t)n_tail * FA_BQ * FA_D, 256));
+        fa_merge_kernel<<<gm, 256, 0, st>>>(a, n_tail);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         snprintf(hd_cuda_errbuf(), 512, "hd_sdpa: flash launch failed: %s", hipGetErrorString(e));
@@ -341,6 +449,19 @@ extern "C" int hd_flash_attention(const void *q, const void *k, const void *vt, 
                      out_seq_major, hd_stream());
 }
 
+extern "C" int hd_flash_attention_ws(const void *q, const void *k, const void *vt, const void *mask,
+                                     void *out, int batch, int q_heads, int kv_heads, int seq,
+                                     int head_dim, int ar_len, float scale, int out_seq_major,
+                                     void *ws, int64_t ws_bytes) {
+    if (!q || !k || !vt || !out || batch <= 0 || q_heads <= 0 || kv_heads <= 0 ||
+        q_heads % kv_heads || seq <= 0 || head_dim != FA_D || ar_len < 0 || ar_len > seq) {
+        snprintf(hd_cuda_errbuf(), 512, "hd_sdpa: flash bad args");
+        return 1;
+    }
+    return fa_launch(q, k, vt, mask, out, batch, q_heads, kv_heads, seq, ar_len, seq, scale,
+                     out_seq_major, hd_stream(), ws, ws_bytes);
+}
+
 // ---------------------------------------------------------------------------
 // Plan API (hd_cudnn_sdpa.h). A plan is shape + split point + a V^T staging
 // buffer allocated once at create time (the reference allocates its cuDNN
@@ -352,6 +473,8 @@ struct hd_sdpa_plan {
     float scale;
     void *vt;
     size_t vt_bytes;
+    void *ws = nullptr;      // tail-split partials (hd_flash_ws_bytes)
+    int64_t ws_bytes = 0;
 };
 
 static int sdpa_err(const char *m) {
@@ -376,6 +499,12 @@ static int plan_new(hd_sdpa_plan **out, int batch, int hq, int hkv, int sq, int 
     if (hipMalloc(&p->vt, p->vt_bytes) != hipSuccess) {
         delete p;
         return sdpa_err("hipMalloc V^T staging failed");
+    }
+    p->ws_bytes = hd_flash_ws_bytes();
+    if (hipMalloc(&p->ws, (size_t)p->ws_bytes) != hipSuccess) {
+        (void)hipFree(p->vt);
+        delete p;
+        return sdpa_err("hipMalloc flash workspace failed");
     }
     *out = p;
     return 0;
@@ -405,6 +534,7 @@ extern "C" int hd_sdpa_create_prod(hd_sdpa_plan **out, int batch, int q_heads, i
 extern "C" void hd_sdpa_destroy(hd_sdpa_plan *p) {
     if (!p) return;
     if (p->vt) (void)hipFree(p->vt);
+    if (p->ws) (void)hipFree(p->ws);
     delete p;
 }
 
@@ -416,7 +546,7 @@ static int plan_run(hd_sdpa_plan *p, const void *q, const void *k, const void *v
                                     (int)fa_spad(p->Skv));
     if (hipGetLastError() != hipSuccess) return sdpa_err("V^T staging launch failed");
     return fa_launch(q, k, p->vt, mask, out, p->B, p->Hq, p->Hkv, p->Sq, ar_len, q_row_end,
-                     p->scale, 0, st);
+                     p->scale, 0, st, p->ws, p->ws_bytes);
 }
 
 extern "C" int hd_sdpa_execute(hd_sdpa_plan *p, const void *q, const void *k, const void *v,

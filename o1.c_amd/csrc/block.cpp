@@ -33,6 +33,8 @@ static inline int64_t al256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 struct BlockScratch {
     void *ln, *qkv, *q, *k, *vt, *attn, *ar, *swi;
     float *cs;
+    void *fa_ws;
+    int64_t fa_ws_bytes;
     int64_t bytes;
 };
 
@@ -56,6 +58,8 @@ static BlockScratch carve(void *base, int batch, int64_t seq, int heads, int kv,
     s.ar = take(M * hidden * 2);
     s.swi = take(M * (int64_t)ff * 2);
     s.cs = with_cs ? (float *)take(seq * (int64_t)hd * 4) : nullptr;   // [seq, hd/2] x (cos,sin)
+    s.fa_ws_bytes = hd_flash_ws_bytes();
+    s.fa_ws = take(s.fa_ws_bytes);                                      // attention tail split
     s.bytes = o;
     return s;
 }
@@ -153,8 +157,8 @@ static hd_status block_core(const void *in, const float *cs, const void *mask, i
         hd_qkv_epilogue(s.qkv, bw->q_norm, bw->k_norm, cs, s.q, s.k, nullptr, s.vt, batch,
                         (int)seq, H, KV, D, eps);
     }
-    if (hd_flash_attention(s.q, s.k, s.vt, mask, s.attn, batch, H, KV, (int)seq, D, ar_len, scale,
-                           1) != 0)
+    if (hd_flash_attention_ws(s.q, s.k, s.vt, mask, s.attn, batch, H, KV, (int)seq, D, ar_len,
+                              scale, 1, s.fa_ws, s.fa_ws_bytes) != 0)
         return launch_status("attention");
     hd_linear_residual(s.attn, bw->o_proj, in, s.ar, M, HID, H * D);
     if (ints && ints->attn_hidden) hd_linear(s.attn, bw->o_proj, nullptr, ints->attn_hidden, M, HID, H * D, 1);

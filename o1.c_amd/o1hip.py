@@ -183,6 +183,9 @@ SIGNATURES = {
     "hd_sdpa_create_prod": (c_int, [ctypes.POINTER(c_void_p), c_int, c_int, c_int, c_int, c_int, c_int, c_float]),
     "hd_flash_attention": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int]),
     "hd_sdpa_plan_ar_len": (c_int, [P]),
+    "hd_flash_attention_ws": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int,
+                                      P, c_int64]),
+    "hd_flash_ws_bytes": (c_int64, []),
     "hd_flash_vt_bytes": (c_int64, [c_int, c_int, c_int]),
     "hd_flash_make_vt": (None, [P, P, c_int, c_int]),
     # hd_weights.h
