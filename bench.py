@@ -292,10 +292,12 @@ def run_c4(pkg, lib, model, tensors, cfg, ws, ids, posd, vin, T, I, S, dev, args
     img_s = e0.elapsed_time(e1) / 1000.0
     zf = z.float()
     assert torch.isfinite(zf).all(), "non-finite latent"
-    return {"lora": {"targets": k, "rank": r, "merge_ms": round(merge_ms, 3),
-                     "weight_elems": welems,
-                     "hbm_gb_s": round(welems * 4 / (merge_ms * 1e-3) / 1e9, 1),
-                     "fp32_tflops": round(welems * 2 * r / (merge_ms * 1e-3) / 1e12, 2)},
+    lora = {"targets": k, "rank": r, "merge_ms": round(merge_ms, 3), "weight_elems": welems,
+            "hbm_gb_s": round(welems * 4 / (merge_ms * 1e-3) / 1e9, 1),
+            "fp32_tflops": round(welems * 2 * r / (merge_ms * 1e-3) / 1e12, 2)}
+    if not args.no_cpu_baseline:
+        lora["cpu_baseline"] = cpu_lora_baseline(r, welems)
+    return {"lora": lora,
             "sampler": {"steps": steps, "guidance": g, "shift": shift,
                         "sigmas_first_last": [round(sch.sigmas[0], 6), round(sch.sigmas[steps - 1], 6)],
                         "s_per_image": round(img_s, 3), "wall_s": round(wall, 3),
@@ -333,6 +335,27 @@ def read_traffic():
     except OSError:
         pass
     return None
+
+
+def cpu_lora_baseline(r, welems):
+    """The fp32 C oracle merging one gate-sized target (12288 x 4096, rank r)
+    on the host cores, extrapolated by element count to the whole merge."""
+    import numpy as np
+    from oracle import oracle as orc
+    threads = min(os.cpu_count() or 1, 16)
+    orc.lib().o1o_set_threads(threads)
+    N, K = FF, HID
+    rng = np.random.default_rng(0)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    up = (rng.standard_normal((N, r)) * 0.01).astype(np.float32)
+    down = (rng.standard_normal((r, K)) * 0.01).astype(np.float32)
+    t0 = time.perf_counter()
+    orc.lora_merge(w, up, down, 1.0)
+    dt = time.perf_counter() - t0
+    return {"value": round(dt * 1e3 * welems / (N * K), 1), "unit": "ms (whole merge)", "cores": threads,
+            "kind": "port",
+            "sample": f"1 target {N}x{K} rank {r} merged by the fp32 C oracle (OpenMP) in {dt:.2f}s, "
+                      f"x {welems / (N * K):.1f} for all targets; cpu={platform.processor() or platform.machine()}"}
 
 
 def cpu_baseline(S, T, gh, gw, B, layers):
