@@ -113,6 +113,18 @@ class hd_lora_entry(ctypes.Structure):
                 ("down_dev", c_void_p), ("up_dev", c_void_p), ("base_dev", c_void_p)]
 
 
+class hd_ref_geom(ctypes.Structure):
+    _fields_ = [(n, c_int) for n in ("tokens", "grid_h", "grid_w", "cond_h", "cond_w")]
+
+
+class hd_sequence(ctypes.Structure):
+    _fields_ = [("input_ids", ctypes.POINTER(ctypes.c_int64)), ("pos_f32", ctypes.POINTER(c_float)),
+                ("mask_bf16", ctypes.POINTER(ctypes.c_uint8)), ("vinput_mask", ctypes.POINTER(ctypes.c_uint8)),
+                ("sec", ctypes.c_int64 * 3), ("text_len", c_int), ("image_len", c_int),
+                ("img_begin", c_int), ("S", c_int), ("n_refs", c_int),
+                ("ref_len", c_int * 20), ("ref_begin", c_int * 20)]
+
+
 P = c_void_p
 # name -> (restype, argtypes); every symbol include/*.h declares.
 SIGNATURES = {
@@ -260,6 +272,14 @@ SIGNATURES = {
                            c_int, c_int, c_int, c_int, P, c_int64, P]),
     "hd_unipc_convert": (None, [P, P, c_float, P, c_int]),
     "hd_unipc_correct": (None, [P, P, P, P] + [c_float] * 8 + [c_int, P, c_int]),
+    # hd_sequence.h
+    "hd_resolution_snap": (None, [c_int, c_int, ctypes.POINTER(c_int), ctypes.POINTER(c_int)]),
+    "hd_seq_t2i": (c_int, [P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                           c_int, ctypes.POINTER(hd_sequence)]),
+    "hd_seq_build_tokens": (c_int, [P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                                    c_int, c_int, c_int, ctypes.POINTER(hd_ref_geom), ctypes.POINTER(hd_sequence)]),
+    "hd_sequence_free": (None, [ctypes.POINTER(hd_sequence)]),
+    "hd_seq_diag": (c_int, [ctypes.POINTER(hd_sequence), c_char_p]),
     "hd_unipc_predict": (None, [P, P, P] + [c_float] * 7 + [c_int, P, c_int]),
 }
 
