@@ -77,8 +77,11 @@ typedef struct {
     void *after_final_head;
 } hd_forward_diagnostics;
 
-/* forward.h:109-115 (vision conditioning: not supported here; a non-NULL
- * `visual` fails closed with HD_ERR_UNSUPPORTED). */
+/* forward.h:127-134: vision conditioning for hd_forward (batch 1). Device
+ * pointers, bf16: image_embeds [v_tokens, hidden] replace the rows whose
+ * visual_mask [S] byte is set, in order (text rows only); deepstack[i]
+ * [v_tokens, hidden] is added to those rows of block i's output, i < 3
+ * (a NULL deepstack[i] skips that layer). */
 typedef struct {
     const void *image_embeds;
     const void *deepstack[3];

@@ -52,6 +52,11 @@ void hd_gemm_set_backend(int use_production);
  * kernel family, so the value is recorded and otherwise ignored. */
 void hd_gemm_set_prod_backend(int backend);
 
+/* Extension: hd_linear (transpose_w = 1) writing rows of stride ldc >= N
+ * (ldc % 8 == 0); columns [N, ldc) are left untouched. */
+void hd_linear_ld(const void *x_dev, const void *w_dev, const void *bias_dev, void *y_dev, int M,
+                  int N, int K, int ldc);
+
 /* ---- fused-epilogue entry points (extension) --------------------------
  * y = bf16(res + bf16(x . W^T))      : residual epilogue (o_proj, down)   */
 void hd_linear_residual(const void *x_dev, const void *w_dev,

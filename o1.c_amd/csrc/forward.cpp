@@ -17,6 +17,7 @@
 #include "../../include/hd_sdpa.h"
 #include "../../include/hd_block.h"
 #include "../../include/hd_forward.h"
+#include "../../include/hd_vision.h"
 
 #define HD_PATCH_FEATS 3072   // forward.c:299-301 (3 x 32 x 32)
 #define HD_XE_MID 1024        // x_embedder bottleneck
@@ -162,7 +163,8 @@ static hd_status forward_core(const hd_forward_binding *bw, hd_forward_workspace
                               const int64_t *ids, int T, const float *pos, const void *mask,
                               int ar_len, const void *vin, int I, const float *tstep, int S,
                               int H, int KV, int HID, int FF, int D, int tms,
-                              hd_forward_diagnostics *dg, void *out) {
+                              hd_forward_diagnostics *dg, void *out,
+                              const hd_visual_cond *vis = nullptr) {
     const hd_block_config *cfg;
     hd_block_config c;
     hd_block_get_config(&c);
@@ -201,6 +203,9 @@ static hd_status forward_core(const hd_forward_binding *bw, hd_forward_workspace
         uint16_t *ht = h_text + (size_t)b * T * HID;
         hd_gather_rows(bw->embed_tokens, ids + (size_t)b * T, ht, T, HID, HD_VOCAB);
         if (dg && b == 0 && (s = d2d(dg->after_embedding, ht, (size_t)T * row, st)) != HD_OK) return s;
+        // vision conditioning (forward.c:278-287): the image-pad rows take the
+        // vision tower's embeddings in order, before the timestep substitution
+        if (vis) hd_vision_masked_scatter_n(ht, vis->visual_mask, vis->image_embeds, ht, T, HID, vis->v_tokens);
         hd_apply_tms_condition(ids + (size_t)b * T, ht, (const uint16_t *)te_h + (size_t)b * HID,
                                hidden + (size_t)b * S * HID, T, HID, tms);
         if (dg && b == 0 &&
@@ -241,6 +246,11 @@ static hd_status forward_core(const hd_forward_binding *bw, hd_forward_workspace
                                              : (i == n - 1 ? dg->after_block_last : nullptr));
             if ((s = d2d(dst, hidden, (size_t)S * row, st)) != HD_OK) return s;
         }
+        // DeepStack (forward.c:363-370): blocks 0..2 add the deepstack
+        // embeddings to the image-pad rows of their output
+        if (vis && i < 3 && vis->deepstack[i])
+            hd_vision_deepstack_inject_n(hidden, vis->visual_mask, vis->deepstack[i], hidden, S, HID,
+                                         vis->v_tokens);
     }
     if (dg && (s = d2d(dg->before_final_norm, hidden, (size_t)S * row, st)) != HD_OK) return s;
     hd_rmsnorm(hidden, bw->fnorm_w, norm_out, B * S, HID, cfg->eps);
@@ -290,9 +300,9 @@ extern "C" hd_status hd_forward(const hd_forward_binding *bw, hd_forward_workspa
         hd_set_error("forward: null argument");
         return HD_ERR_MISSING;
     }
-    if (visual) {
-        hd_set_error("forward: vision conditioning is not supported by this build");
-        return HD_ERR_UNSUPPORTED;
+    if (visual && (!visual->image_embeds || !visual->visual_mask || visual->v_tokens < 0)) {
+        hd_set_error("forward: visual conditioning without embeddings or mask");
+        return HD_ERR_MISSING;
     }
     hd_status s = common_checks(bw, ws, text_len, img_tokens, seq, heads, kv_heads, hidden,
                                 ff_hidden, head_dim);
@@ -302,7 +312,7 @@ extern "C" hd_status hd_forward(const hd_forward_binding *bw, hd_forward_workspa
     const void *mask = ar_len > 0 ? nullptr : mask_dev;
     return forward_core(bw, ws, 1, input_ids, text_len, pos_f32, mask, ar_len, vinputs, img_tokens,
                         timestep, seq, heads, kv_heads, hidden, ff_hidden, head_dim, tms_token_id,
-                        diag, out_dev);
+                        diag, out_dev, visual);
 }
 
 extern "C" hd_status hd_forward_batched(const hd_forward_binding *bw, hd_forward_workspace *ws,

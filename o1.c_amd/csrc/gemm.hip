@@ -1316,6 +1316,26 @@ extern "C" void hd_linear(const void *x, const void *w, const void *bias, void *
     hd_check_launch("linear");
 }
 
+// hd_linear writing rows of stride ldc (>= N, ldc % 8 == 0): the vision
+// tower's fc1 lands in a row padded to the next GEMM's K.
+extern "C" void hd_linear_ld(const void *x, const void *w, const void *bias, void *y, int M, int N,
+                             int K, int ldc) {
+    if (!x || !w || !y || M <= 0 || N <= 0 || K <= 0 || ldc < N || ldc % 8 || !mfma_ok(x, y, N, K) ||
+        (bias && (uintptr_t)bias % 16)) {
+        snprintf(hd_cuda_errbuf(), 512, "linear_ld: bad args");
+        return;
+    }
+    GemmArgs g = {};
+    g.A = (const uint16_t *)x;
+    g.B[0] = g.B[1] = g.B[2] = (const uint16_t *)w;
+    g.seg_end[0] = g.seg_end[1] = g.seg_end[2] = N;
+    g.C = (uint16_t *)y;
+    g.bias = (const uint16_t *)bias;
+    g.M = M; g.N = N; g.K = K; g.ldc = ldc;
+    gemm_launch(bias ? EPI_BIAS : EPI_NONE, g);
+    hd_check_launch("linear_ld");
+}
+
 extern "C" void hd_linear_residual(const void *x, const void *w, const void *res, void *y, int M,
                                    int N, int K) {
     if (!x || !w || !res || !y || M <= 0 || N <= 0 || K <= 0 || !mfma_ok(x, y, N, K) ||

@@ -125,6 +125,49 @@ class hd_sequence(ctypes.Structure):
                 ("ref_len", c_int * 20), ("ref_begin", c_int * 20)]
 
 
+class hd_vision_block_binding(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in ("norm1_w", "norm1_b", "norm2_w", "norm2_b", "qkv_w", "qkv_b",
+                                        "proj_w", "proj_b", "fc1_w", "fc1_b", "fc2_w", "fc2_b")]
+
+
+class hd_vision_merger_binding(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in ("norm_w", "norm_b", "fc1_w", "fc1_b", "fc2_w", "fc2_b")]
+
+
+class hd_vision_binding(ctypes.Structure):
+    _fields_ = [("patch_proj_w", c_void_p), ("patch_proj_b", c_void_p), ("pos_embed", c_void_p),
+                ("blocks", hd_vision_block_binding * 27), ("merger", hd_vision_merger_binding),
+                ("deepstack", hd_vision_merger_binding * 3)]
+
+
+VISION_WS_BUFFERS = ("patch_out", "pos_emb", "rot", "cosf", "sinf", "h_a", "h_b", "ln1", "qkv", "q",
+                     "k", "v", "qr", "kr", "scores", "probs", "attn_out", "attn_resid", "ln2", "fc1",
+                     "fc2", "mlp_resid", "merged", "merge_norm", "merge_fc1", "merge_fc2",
+                     "ds_merged", "ds_fc1", "ds_fc2")
+
+
+class hd_vision_workspace(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in VISION_WS_BUFFERS] + \
+               [(n, c_void_p) for n in ("pos_idx", "pos_wgt", "rot_coords", "rot_inv", "tables")] + \
+               [("tables_n", c_int), ("tables_gh", c_int), ("tables_gw", c_int),
+                ("bytes", ctypes.c_int64), ("sdpa", c_void_p), ("block0_snap", c_void_p),
+                ("block0_snaps", c_void_p * 16), ("block_out_snaps", c_void_p * 27),
+                ("merger_snaps", c_void_p * 5), ("ds_merger_snaps", (c_void_p * 4) * 3)]
+
+
+class hd_vision_offsets(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int64) for n in (
+        "patch_out", "pos_emb", "rot", "h_a", "h_b", "ln1", "attn_resid", "ln2", "fc2", "mlp_resid",
+        "q", "k", "v", "qr", "kr", "qkv", "scores", "probs", "mask", "attn_out", "fc1", "cosf",
+        "sinf", "merged", "merge_norm", "merge_fc1", "merge_fc2", "ds_merged", "ds_fc1", "ds_fc2",
+        "total_bytes")]
+
+
+class hd_visual_cond(ctypes.Structure):
+    _fields_ = [("image_embeds", c_void_p), ("deepstack", c_void_p * 3), ("visual_mask", c_void_p),
+                ("v_tokens", c_int)]
+
+
 P = c_void_p
 # name -> (restype, argtypes); every symbol include/*.h declares.
 SIGNATURES = {
@@ -280,6 +323,29 @@ SIGNATURES = {
                                     c_int, c_int, c_int, ctypes.POINTER(hd_ref_geom), ctypes.POINTER(hd_sequence)]),
     "hd_sequence_free": (None, [ctypes.POINTER(hd_sequence)]),
     "hd_seq_diag": (c_int, [ctypes.POINTER(hd_sequence), c_char_p]),
+    # hd_vision.h
+    "hd_vision_layout": (None, [ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(hd_vision_offsets)]),
+    "hd_vision_resolve": (c_int, [ctypes.POINTER(hd_weight_store), ctypes.POINTER(hd_vision_binding)]),
+    "hd_vision_workspace_bytes": (ctypes.c_int64, [ctypes.c_int64]),
+    "hd_vision_tables_bytes": (ctypes.c_int64, [ctypes.c_int64]),
+    "hd_vision_prepare_tables": (c_int, [ctypes.POINTER(hd_vision_workspace), c_int, c_int, c_int]),
+    "hd_vision_forward": (c_int, [ctypes.POINTER(hd_vision_binding), ctypes.POINTER(hd_vision_workspace),
+                                  P, c_int, c_int, c_int, P, ctypes.POINTER(P)]),
+    "hd_vision_patch": (None, [P, P, P, P, c_int, c_int, c_int]),
+    "hd_vision_layernorm": (None, [P, P, P, P, c_int, c_int, c_float]),
+    "hd_vision_gelu": (None, [P, P, c_size_t]),
+    "hd_vision_gelu_exact": (None, [P, P, c_size_t]),
+    "hd_vision_pos_interp": (None, [P, P, P, P, c_int, c_int]),
+    "hd_vision_rot": (None, [P, P, P, c_int, c_int]),
+    "hd_vision_rot_cos_sin": (None, [P, P, P, c_int, c_int]),
+    "hd_vision_spatial_merge": (None, [P, P, c_int, c_int, c_int]),
+    "hd_vision_qkv_split": (None, [P, P, P, P, c_int, c_int, c_int]),
+    "hd_vision_attn_merge": (None, [P, P, c_int, c_int, c_int]),
+    "hd_vision_masked_scatter": (None, [P, P, P, P, c_int, c_int]),
+    "hd_vision_deepstack_inject": (None, [P, P, P, P, c_int, c_int]),
+    "hd_vision_masked_scatter_n": (None, [P, P, P, P, c_int, c_int, c_int]),
+    "hd_vision_deepstack_inject_n": (None, [P, P, P, P, c_int, c_int, c_int]),
+    "hd_linear_ld": (None, [P, P, P, P, c_int, c_int, c_int, c_int]),
     "hd_unipc_predict": (None, [P, P, P] + [c_float] * 7 + [c_int, P, c_int]),
 }
 

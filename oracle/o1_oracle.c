@@ -361,9 +361,14 @@ int o1o_decoder_block(const float *x, const float *pos, const float *mask,
 }
 
 /* forward.c:253-397 for one sequence. */
-int o1o_forward(const o1o_forward_weights *w, const o1o_block_cfg *c, const int64_t *ids, int T,
-                const float *vin, int I, float t, const float *pos, const float *mask,
-                int64_t tms_id, float *out, float *after_blocks) {
+/* forward.c:278-287 + :363-370 when vmask != NULL: text rows whose vmask
+ * byte is set take image_embeds rows in order (before the timestep-token
+ * substitution); after block l < 3, deepstack[l] (if non-NULL) is added to
+ * the set rows of the block output with one bf16 rounding. */
+int o1o_forward_visual(const o1o_forward_weights *w, const o1o_block_cfg *c, const int64_t *ids,
+                       int T, const float *vin, int I, float t, const float *pos, const float *mask,
+                       int64_t tms_id, const float *image_embeds, const float *const *deepstack,
+                       const uint8_t *vmask, float *out, float *after_blocks) {
     const int HID = c->hidden, S = T + I, R = c->faithful;
     const int lmode = R ? 2 : 0;
     float *h = malloc(sizeof(float) * (size_t)S * HID);
@@ -387,6 +392,11 @@ int o1o_forward(const o1o_forward_weights *w, const o1o_block_cfg *c, const int6
             if (id < 0 || id >= w->vocab) id = 0;
             src = w->embed_tokens + (size_t)id * HID;
         }
+        if (vmask && vmask[i] && id != tms_id) {
+            int r = 0;
+            for (int j = 0; j < i; j++) r += vmask[j] != 0;
+            src = image_embeds + (size_t)r * HID;
+        }
         memcpy(h + (size_t)i * HID, src, sizeof(float) * HID);
     }
     if (I > 0) {                                                   /* :301-313 */
@@ -399,12 +409,28 @@ int o1o_forward(const o1o_forward_weights *w, const o1o_block_cfg *c, const int6
             return -1;
         }
         float *sw = h; h = h2; h2 = sw;
+        if (vmask && l < 3 && deepstack && deepstack[l]) {
+            int r = 0;
+            for (int i = 0; i < S; i++) {
+                if (!vmask[i]) continue;
+                for (int j = 0; j < HID; j++)
+                    h[(size_t)i * HID + j] = rnd(h[(size_t)i * HID + j] + deepstack[l][(size_t)r * HID + j], R);
+                r++;
+            }
+        }
         if (after_blocks) memcpy(after_blocks + (size_t)l * S * HID, h, sizeof(float) * (size_t)S * HID);
     }
     o1o_rmsnorm(h, w->fnorm_w, h2, S, HID, c->eps, R);             /* :388 */
     o1o_linear(h2, w->fl_w, w->fl_b, out, S, 3072, HID, lmode);    /* :396 */
     free(h); free(h2); free(xs); free(th); free(temb);
     return 0;
+}
+
+int o1o_forward(const o1o_forward_weights *w, const o1o_block_cfg *c, const int64_t *ids, int T,
+                const float *vin, int I, float t, const float *pos, const float *mask,
+                int64_t tms_id, float *out, float *after_blocks) {
+    return o1o_forward_visual(w, c, ids, T, vin, I, t, pos, mask, tms_id, NULL, NULL, NULL, out,
+                              after_blocks);
 }
 
 /* lora_merge.cu:26-104 */

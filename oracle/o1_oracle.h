@@ -96,6 +96,12 @@ int o1o_forward(const o1o_forward_weights *w, const o1o_block_cfg *cfg, const in
                 const float *vin, int I, float t, const float *pos, const float *mask,
                 int64_t tms_id, float *out, float *after_blocks);
 
+/* o1o_forward with vision conditioning (forward.c:278-287, :363-370):
+ * vmask [S] bytes, image_embeds [V, hidden], deepstack[3] [V, hidden]. */
+int o1o_forward_visual(const o1o_forward_weights *w, const o1o_block_cfg *cfg, const int64_t *ids,
+                       int T, const float *vin, int I, float t, const float *pos, const float *mask,
+                       int64_t tms_id, const float *image_embeds, const float *const *deepstack,
+                       const uint8_t *vmask, float *out, float *after_blocks);
 /* lora_merge.cu:26-104: W = bf16(W + scale * up[N,R] @ down[R,K]) */
 void o1o_lora_merge(float *w, const float *up, const float *down, int N, int K, int R, float scale);
 

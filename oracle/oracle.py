@@ -37,6 +37,27 @@ class ForwardWeights(ctypes.Structure):
                 ("blocks", ctypes.POINTER(BlockWeights))]
 
 
+class VisionBlock(ctypes.Structure):
+    _fields_ = [(n, F) for n in ("norm1_w", "norm1_b", "norm2_w", "norm2_b", "qkv_w", "qkv_b",
+                                 "proj_w", "proj_b", "fc1_w", "fc1_b", "fc2_w", "fc2_b")]
+
+
+class VisionMerger(ctypes.Structure):
+    _fields_ = [(n, F) for n in ("norm_w", "norm_b", "fc1_w", "fc1_b", "fc2_w", "fc2_b")]
+
+
+class VisionWeights(ctypes.Structure):
+    _fields_ = [("patch_w", F), ("patch_b", F), ("pos_embed", F),
+                ("blocks", ctypes.POINTER(VisionBlock)), ("merger", VisionMerger),
+                ("deepstack", VisionMerger * 4)]
+
+
+class VisionCfg(ctypes.Structure):
+    _fields_ = [(n, c_int) for n in ("depth", "hidden", "heads", "inter", "out_hidden",
+                                     "patch_dim", "nside", "merge", "n_ds")] + \
+               [("ds_layers", c_int * 4), ("faithful", c_int)]
+
+
 def lib():
     global _lib
     if _lib is None:
@@ -64,6 +85,10 @@ def lib():
         L.o1o_forward.restype = c_int
         L.o1o_forward.argtypes = [ctypes.POINTER(ForwardWeights), ctypes.POINTER(BlockCfg), I64,
                                   c_int, F, c_int, c_float, F, F, c_int64, F, F]
+        L.o1o_forward_visual.restype = c_int
+        L.o1o_forward_visual.argtypes = [ctypes.POINTER(ForwardWeights), ctypes.POINTER(BlockCfg),
+                                         I64, c_int, F, c_int, c_float, F, F, c_int64, F,
+                                         ctypes.POINTER(F), ctypes.POINTER(ctypes.c_uint8), F, F]
         L.o1o_lora_merge.argtypes = [F, F, F, c_int, c_int, c_int, c_float]
         L.o1o_sched_vcond.argtypes = [F, F, c_float, F, c_int]
         L.o1o_sched_flow_match_step.argtypes = [F, F, c_float, c_float, F, c_int]
@@ -73,6 +98,15 @@ def lib():
         L.o1o_unipc_predict.argtypes = [F, F, F] + [c_float] * 7 + [c_int, F, c_int]
         L.o1o_patchify.argtypes = [F, F, c_int, c_int, c_int, c_int]
         L.o1o_unpatchify.argtypes = [F, F, c_int, c_int, c_int, c_int]
+        L.o1o_layernorm.argtypes = [F, F, F, F, c_int, c_int, c_float, c_int]
+        L.o1o_gelu_tanh.argtypes = [F, F, c_size_t, c_int]
+        L.o1o_gelu_erf.argtypes = [F, F, c_size_t, c_int]
+        IP = ctypes.POINTER(c_int)
+        L.o1o_vision_tables.argtypes = [c_int, c_int, c_int, c_int, IP, F, IP]
+        L.o1o_vision_rotary.argtypes = [IP, c_int, c_int, c_int, F, F]
+        L.o1o_vision_forward.restype = c_int
+        L.o1o_vision_forward.argtypes = [ctypes.POINTER(VisionWeights), ctypes.POINTER(VisionCfg), F,
+                                         c_int, c_int, F, ctypes.POINTER(F), F]
         L.o1o_decode_to_rgb.argtypes = [F, c_int, c_int, c_int, c_int,
                                         ctypes.POINTER(ctypes.c_uint8)]
     return _lib
@@ -206,8 +240,9 @@ def decoder_block(x, pos, w, cfg, batch=1, mask=None, internals=False):
     return (out, *ints) if internals else out
 
 
-def forward(fw, cfg, ids, vin, t, pos, tms_id, mask=None, keep_blocks=False):
-    """fw: dict of global arrays + 'blocks' list of per-layer dicts."""
+def forward(fw, cfg, ids, vin, t, pos, tms_id, mask=None, keep_blocks=False, visual=None):
+    """fw: dict of global arrays + 'blocks' list of per-layer dicts.
+    visual: optional (image_embeds [V,hidden], [deepstack0..2 or None], vmask [S] uint8)."""
     keep = []
     blocks = (BlockWeights * len(fw["blocks"]))()
     for i, bwd in enumerate(fw["blocks"]):
@@ -226,9 +261,22 @@ def forward(fw, cfg, ids, vin, t, pos, tms_id, mask=None, keep_blocks=False):
     S = T + I
     out = np.empty((S, 3072), np.float32)
     ab = np.empty((len(fw["blocks"]), S, cfg.hidden), np.float32) if keep_blocks else None
-    rc = lib().o1o_forward(ctypes.byref(W), ctypes.byref(cfg),
-                           ids.ctypes.data_as(I64), T, fp(vin), I, float(t), fp(f32(pos)),
-                           fp(None if mask is None else f32(mask)), tms_id, fp(out), fp(ab))
+    if visual is None:
+        rc = lib().o1o_forward(ctypes.byref(W), ctypes.byref(cfg),
+                               ids.ctypes.data_as(I64), T, fp(vin), I, float(t), fp(f32(pos)),
+                               fp(None if mask is None else f32(mask)), tms_id, fp(out), fp(ab))
+    else:
+        emb = f32(visual[0])
+        ds = [None if d is None else f32(d) for d in visual[1]] + [None] * (3 - len(visual[1]))
+        dsp = (F * 3)(*[fp(d) for d in ds])
+        vm = np.ascontiguousarray(visual[2], dtype=np.uint8)
+        keep.append((emb, ds, vm))
+        rc = lib().o1o_forward_visual(ctypes.byref(W), ctypes.byref(cfg),
+                                      ids.ctypes.data_as(I64), T, fp(vin), I, float(t),
+                                      fp(f32(pos)), fp(None if mask is None else f32(mask)),
+                                      tms_id, fp(emb), dsp,
+                                      vm.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), fp(out),
+                                      fp(ab))
     assert rc == 0
     return (out, ab) if keep_blocks else out
 
@@ -308,3 +356,90 @@ def sched_cfg_guided(c, u, g):
     o = np.empty_like(c)
     lib().o1o_sched_cfg_guided(fp(c), fp(u), g, fp(o), c.size)
     return o
+
+
+# ---- vision tower (o1_vision.c) -------------------------------------------
+VISION_BLOCK_KEYS = ("norm1.weight", "norm1.bias", "norm2.weight", "norm2.bias", "attn.qkv.weight",
+                     "attn.qkv.bias", "attn.proj.weight", "attn.proj.bias",
+                     "mlp.linear_fc1.weight", "mlp.linear_fc1.bias", "mlp.linear_fc2.weight",
+                     "mlp.linear_fc2.bias")
+VISION_MERGER_KEYS = ("norm.weight", "norm.bias", "linear_fc1.weight", "linear_fc1.bias",
+                      "linear_fc2.weight", "linear_fc2.bias")
+
+
+def layernorm(x, w, b, eps=1e-6, round_=1):
+    x = f32(x)
+    y = np.empty_like(x)
+    lib().o1o_layernorm(fp(x), fp(f32(w)), fp(f32(b)) if b is not None else None, fp(y),
+                        x.shape[0], x.shape[1], eps, round_)
+    return y
+
+
+def gelu_tanh(x, round_=1):
+    x = f32(x)
+    y = np.empty_like(x)
+    lib().o1o_gelu_tanh(fp(x), fp(y), x.size, round_)
+    return y
+
+
+def gelu_erf(x, round_=1):
+    x = f32(x)
+    y = np.empty_like(x)
+    lib().o1o_gelu_erf(fp(x), fp(y), x.size, round_)
+    return y
+
+
+def vision_tables(gh, gw, nside, merge=2):
+    n = gh * gw
+    idx = np.empty((4, n), np.int32)
+    wgt = np.empty((4, n), np.float32)
+    co = np.empty((2, n), np.int32)
+    IP = ctypes.POINTER(c_int)
+    lib().o1o_vision_tables(gh, gw, nside, merge, idx.ctypes.data_as(IP), fp(wgt),
+                            co.ctypes.data_as(IP))
+    return idx, wgt, co
+
+
+def vision_forward(w, pixels, gh, gw, depth, heads, ds_layers, faithful=1, merge=2,
+                   keep_blocks=False):
+    """w: dict of the vision tower's tensors under their checkpoint names
+    without the 'model.visual.' prefix (patch_embed.proj.weight as
+    [hidden, patch_dim]). Returns (embeds, [deepstack...]) and, with
+    keep_blocks, the [depth, n, hidden] block outputs."""
+    keep = []
+
+    def a(name):
+        arr = f32(w[name])
+        keep.append(arr)
+        return fp(arr)
+
+    blocks = (VisionBlock * depth)()
+    for i in range(depth):
+        blocks[i] = VisionBlock(*[a(f"blocks.{i}.{k}") for k in VISION_BLOCK_KEYS])
+    vw = VisionWeights()
+    vw.patch_w, vw.patch_b, vw.pos_embed = (a("patch_embed.proj.weight"), a("patch_embed.proj.bias"),
+                                            a("pos_embed.weight"))
+    vw.blocks = ctypes.cast(blocks, ctypes.POINTER(VisionBlock))
+    vw.merger = VisionMerger(*[a(f"merger.{k}") for k in VISION_MERGER_KEYS])
+    for j in range(len(ds_layers)):
+        vw.deepstack[j] = VisionMerger(*[a(f"deepstack_merger_list.{j}.{k}") for k in VISION_MERGER_KEYS])
+    H = w["patch_embed.proj.weight"].shape[0]
+    c = VisionCfg()
+    c.depth, c.hidden, c.heads = depth, H, heads
+    c.inter = w["blocks.0.mlp.linear_fc1.weight"].shape[0]
+    c.out_hidden = w["merger.linear_fc2.weight"].shape[0]
+    c.patch_dim = w["patch_embed.proj.weight"].shape[1]
+    c.nside = int(round(w["pos_embed.weight"].shape[0] ** 0.5))
+    c.merge, c.n_ds, c.faithful = merge, len(ds_layers), faithful
+    for j, L in enumerate(ds_layers):
+        c.ds_layers[j] = L
+    m = gh * gw // (merge * merge)
+    emb = np.empty((m, c.out_hidden), np.float32)
+    ds = [np.empty((m, c.out_hidden), np.float32) for _ in ds_layers]
+    dsp = (F * max(1, len(ds)))(*[fp(d) for d in ds])
+    px = f32(pixels)
+    ab = np.empty((depth, gh * gw, H), np.float32) if keep_blocks else None
+    rc = lib().o1o_vision_forward(ctypes.byref(vw), ctypes.byref(c), fp(px), gh, gw, fp(emb),
+                                  dsp if ds else None, fp(ab))
+    assert rc == 0
+    return (emb, ds, ab) if keep_blocks else (emb, ds)
