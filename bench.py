@@ -54,6 +54,9 @@ def main():
     ap.add_argument("--layers", type=int, default=L)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=20)
+    ap.add_argument("--vision-only", action="store_true",
+                    help="run only the vision tower of configuration 3 (3 references of 24x24 "
+                         "patches, one multi-image call, 10 untimed + 10 timed), for rocprofv3")
     ap.add_argument("--kernel-only", action="store_true",
                     help="run only the dominant kernel (gate/up GEMM + SwiGLU at the step's "
                          "shape) and a 1 GiB device copy, for rocprofv3 counter passes")
@@ -80,6 +83,13 @@ def main():
     pkg.bind_torch_stream()
     if args.kernel_only:
         kernel_only(pkg, lib, B * S, args.kernel_iters)
+        return
+    if args.vision_only:
+        from importlib import import_module as _im
+        vids = torch.zeros(1, 512, dtype=torch.int64, device=dev)
+        _, info = run_vision(pkg, lib, _im("o1c_amd.synthetic"), vids, 3, 512, 512 + 3 * 4096, dev,
+                             iters=10)
+        print(json.dumps(info))
         return
     print(f"[bench] building {args.layers}-layer synthetic model", file=sys.stderr, flush=True)
     tensors = synth.build_model(n_layers=args.layers, seed=0, device="cuda:0")
@@ -122,11 +132,22 @@ def main():
         ws.n_ref = n_ref
     if args.config == "c4":
         extra = run_c4(pkg, lib, model, tensors, cfg, ws, ids, posd, vin, T, I, S, dev, args)
+    vis = None
+    if R:
+        vis, extra = run_vision(pkg, lib, synth, ids, R, T, S, dev)
 
     def step():
-        st = lib.hd_forward_batched(ctypes.byref(model.binding), ctypes.byref(ws), B, pkg.ptr(ids), T,
-                                    pkg.ptr(posd), 0, pkg.ptr(vin), I, pkg.ptr(tsd), S, NH, NKV,
-                                    HID, FF, D, synth.TMS_ID, None, pkg.ptr(out), None)
+        if vis is not None:
+            # edit step: vision conditioning on the text rows (image pads
+            # replaced, DeepStack into blocks 0-2) through hd_forward
+            st = lib.hd_forward(ctypes.byref(model.binding), ctypes.byref(ws), pkg.ptr(ids), T,
+                                pkg.ptr(posd), None, pkg.ptr(vin), I, ctypes.addressof(vis["cond"]),
+                                pkg.ptr(tsd), None, S, NH, NKV, HID, FF, D, synth.TMS_ID, None,
+                                pkg.ptr(out), None)
+        else:
+            st = lib.hd_forward_batched(ctypes.byref(model.binding), ctypes.byref(ws), B, pkg.ptr(ids),
+                                        T, pkg.ptr(posd), 0, pkg.ptr(vin), I, pkg.ptr(tsd), S, NH,
+                                        NKV, HID, FF, D, synth.TMS_ID, None, pkg.ptr(out), None)
         if st != 0:
             raise RuntimeError(lib.hd_last_error().decode())
 
@@ -227,6 +248,70 @@ def main():
     }
     res.update(extra)
     print(json.dumps(res))
+
+
+def run_vision(pkg, lib, synth, ids, R, T, S, dev, iters=5):
+    """Reference images through the Qwen3-VL vision tower: R condition
+    images of 384x384 (24x24 patches of 16 px, 144 merged tokens each,
+    generate.c:65, :313-330), random-init tower weights, N(0,1) patchified
+    pixels. The text rows get R x (vision_start, 144 image pads, vision_end)
+    after a 3-token header; the tower runs once per image (before the
+    steps) and its embeddings condition every step."""
+    import torch
+    gh = gw = 24
+    n, m = gh * gw, gh * gw // 4
+    V = R * m
+    print(f"[bench] vision tower: {R} references of {n} patches", file=sys.stderr, flush=True)
+    vt = synth.build_vision(seed=3, device="cuda:0")
+    # all R references in one hd_vision_forward_multi call (same grid)
+    tower = synth.VisionTower(vt, gh, gw, images=R)
+    g = torch.Generator(device=dev).manual_seed(11)
+    px = torch.randn(R * n, synth.V_PATCH, device=dev, generator=g).to(torch.bfloat16)
+    emb = torch.empty(V, synth.V_OUT, dtype=torch.bfloat16, device=dev)
+    ds = [torch.empty(V, synth.V_OUT, dtype=torch.bfloat16, device=dev) for _ in range(3)]
+
+    def run_all():
+        tower(px, emb, ds)
+
+    run_all()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        run_all()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_ref = e0.elapsed_time(e1) / iters / R
+    assert torch.isfinite(emb.float()).all()
+    # text rows: header(3) | R x (vs, m pads, vend) | caption ... | tms
+    VS, PAD, VEND = 151652, 151655, 151653
+    ids_h = ids[0].cpu()
+    vmask = torch.zeros(S, dtype=torch.uint8)
+    at = 3
+    for r in range(R):
+        ids_h[at] = VS
+        ids_h[at + 1:at + 1 + m] = PAD
+        vmask[at + 1:at + 1 + m] = 1
+        ids_h[at + 1 + m] = VEND
+        at += m + 2
+    assert at < T - 1 and int(vmask.sum()) == V
+    ids[0].copy_(ids_h)
+    vmd = vmask.to(dev)
+    cond = pkg.hd_visual_cond()
+    cond.image_embeds = emb.data_ptr()
+    for j in range(3):
+        cond.deepstack[j] = ds[j].data_ptr()
+    cond.visual_mask = vmd.data_ptr()
+    cond.v_tokens = V
+    fl = synth.vision_flops(n)
+    keep = {"cond": cond, "tensors": vt, "tower": tower, "emb": emb, "ds": ds, "vmask": vmd, "px": px}
+    info = {"vision": {"kernel": "vision tower (27 blocks + 4 mergers), R references per call",
+                       "patches": n, "merged_tokens": m, "references": R,
+                       "ms_per_reference": round(ms_ref, 3),
+                       "tflops": round(fl / (ms_ref * 1e-3) / 1e12, 1),
+                       "frac": round(fl / (ms_ref * 1e-3) / PEAK_BF16, 4),
+                       "gflop_per_reference": round(fl / 1e9, 1)}}
+    return keep, info
 
 
 def run_c4(pkg, lib, model, tensors, cfg, ws, ids, posd, vin, T, I, S, dev, args):

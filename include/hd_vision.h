@@ -145,6 +145,20 @@ hd_status hd_vision_forward(const hd_vision_binding *bw, hd_vision_workspace *ws
                             const void *pixel_values, int n, int grid_h, int grid_w,
                             void *image_embeds_out, void *deepstack_out[HD_VISION_NUM_DS]);
 
+/* Extension: `images` reference images of the same grid in one call
+ * (pixel_values [images*n, 1536], image_embeds_out [images*n/4, 4096] and
+ * each deepstack_out [images*n/4, 4096], images in order: the row layout
+ * hd_visual_cond takes for several references). GEMMs and elementwise
+ * kernels run over all rows at once, attention per image; each image's
+ * rows equal what hd_vision_forward computes for it alone. The workspace
+ * is hd_vision_workspace_bytes_multi(images, n) bytes; the tables are the
+ * single-image ones for (n, grid_h, grid_w). */
+hd_status hd_vision_forward_multi(const hd_vision_binding *bw, hd_vision_workspace *ws,
+                                  const void *pixel_values, int images, int n, int grid_h,
+                                  int grid_w, void *image_embeds_out,
+                                  void *deepstack_out[HD_VISION_NUM_DS]);
+int64_t hd_vision_workspace_bytes_multi(int images, int64_t n);
+
 /* ---- kernels (src/cuda/vision_kernels.h) ------------------------------ */
 /* patch embed as GEMM + bias: y [n, out_dim] = x [n, in_dim] . w^T + b */
 void hd_vision_patch(const void *x, const void *w, const void *bias, void *y, int n, int in_dim,

@@ -132,12 +132,13 @@ __global__ void v_gelu_flat_kernel(const uint16_t *__restrict__ x, uint16_t *__r
 // the sum (patch is then not read).
 __global__ void v_embed_kernel(const uint16_t *__restrict__ patch, const uint16_t *__restrict__ pe,
                                const int *__restrict__ idx, const float *__restrict__ wgt,
-                               uint16_t *__restrict__ pos_out, uint16_t *__restrict__ h, int n,
-                               int hidden) {
+                               uint16_t *__restrict__ pos_out, uint16_t *__restrict__ h, int rows,
+                               int n, int hidden) {
     const int cpr = hidden >> 3;
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)n * cpr) return;
-    const int row = (int)(i / cpr), c = (int)(i % cpr) * 8;
+    if (i >= (size_t)rows * cpr) return;
+    const int grow = (int)(i / cpr), c = (int)(i % cpr) * 8;
+    const int row = grow % n;                  // tables are per image of n patches
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int t = 0; t < 4; t++) {
@@ -150,7 +151,7 @@ __global__ void v_embed_kernel(const uint16_t *__restrict__ patch, const uint16_
         }
     }
     u32x4_t pv = {0, 0, 0, 0};
-    if (h) pv = *(const u32x4_t *)(patch + (size_t)row * hidden + c);
+    if (h) pv = *(const u32x4_t *)(patch + (size_t)grow * hidden + c);
     u32x4_t o, po;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -158,8 +159,8 @@ __global__ void v_embed_kernel(const uint16_t *__restrict__ patch, const uint16_
         po[j] = pack_bf2(p0, p1);
         o[j] = pack_bf2(lo_bf(pv[j]) + p0, hi_bf(pv[j]) + p1);
     }
-    if (pos_out) *(u32x4_t *)(pos_out + (size_t)row * hidden + c) = po;
-    if (h) *(u32x4_t *)(h + (size_t)row * hidden + c) = o;
+    if (pos_out) *(u32x4_t *)(pos_out + (size_t)grow * hidden + c) = po;
+    if (h) *(u32x4_t *)(h + (size_t)grow * hidden + c) = o;
 }
 
 // Rotary tables (vision.c:415-420, vision_kernels.cu:183-231): angle
@@ -194,18 +195,19 @@ __global__ void v_cos_sin_kernel(const uint16_t *__restrict__ rot, float *__rest
     sind[(size_t)s * 2 * half + k] = sind[(size_t)s * 2 * half + half + k] = sn;
 }
 
-// qkv [n, 3, heads, D] -> q, k (rotary applied in fp32, one rounding,
-// rope.cu:157-180) and v, head-major [heads, n, DP] with columns [D, DP)
-// zero: the flash kernel's head_dim-128 operands. One thread per output
-// element of q, k and v.
+// qkv [R*n, 3, heads, D] (R images of n rows) -> q, k (rotary applied in
+// fp32, one rounding, rope.cu:157-180) and v, head-major [R, heads, n, DP]
+// with columns [D, DP) zero: the flash kernel's head_dim-128 operands. One
+// thread per output element of q, k and v.
 __global__ void v_qkv_rope_pad_kernel(const uint16_t *__restrict__ qkv, const float *__restrict__ cosd,
                                       const float *__restrict__ sind, uint16_t *__restrict__ q,
-                                      uint16_t *__restrict__ k, uint16_t *__restrict__ v, int n,
-                                      int heads, int D, int DP) {
+                                      uint16_t *__restrict__ k, uint16_t *__restrict__ v, int R,
+                                      int n, int heads, int D, int DP) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)heads * n * DP) return;
+    if (i >= (size_t)R * heads * n * DP) return;
     const int d = (int)(i % DP);
-    const int s = (int)((i / DP) % n), h = (int)(i / ((size_t)DP * n));
+    const int s = (int)((i / DP) % n), h = (int)((i / ((size_t)DP * n)) % heads);
+    const int img = (int)(i / ((size_t)DP * n * heads));
     if (d >= D) {
         q[i] = 0;
         k[i] = 0;
@@ -213,7 +215,7 @@ __global__ void v_qkv_rope_pad_kernel(const uint16_t *__restrict__ qkv, const fl
         return;
     }
     const int half = D / 2, dp = d < half ? d + half : d - half;
-    const size_t row = (size_t)s * 3 * heads * D;
+    const size_t row = ((size_t)img * n + s) * 3 * heads * D;
     const float c = cosd[(size_t)s * D + d], sn = sind[(size_t)s * D + d];
     const uint16_t *qs = qkv + row + (size_t)h * D, *ks = qs + (size_t)heads * D;
     const float q0 = bf2f(qs[d]), qh = bf2f(qs[dp]), k0 = bf2f(ks[d]), kh = bf2f(ks[dp]);
@@ -354,20 +356,24 @@ struct Layout {
 
 int64_t al(int64_t b) { return (b + 255) & ~(int64_t)255; }
 
-Layout layout_of(int64_t n) {
+// R images of n patches each
+Layout layout_of(int64_t R, int64_t n) {
     Layout L;
     int64_t b = 0;
-    const int64_t nr = n + 128;   // head rows padded: the flash kernel reads whole 128-row tiles
-    L.tmp = b; b += al(n * kH * 2);
-    L.h = b; b += al(n * kH * 2);
-    L.ar = b; b += al(n * kH * 2);
-    L.ln = b; b += al(n * kH * 2);
-    L.qkv = b; b += al(n * (kQKV > kNH * kDP ? kQKV : kNH * kDP) * 2);
-    L.q = b; b += al(kNH * nr * kDP * 2);
-    L.k = b; b += al(kNH * nr * kDP * 2);
-    L.v = b; b += al(kNH * nr * kDP * 2);
-    L.vt = b; b += al(hd_flash_vt_bytes(1, kNH, (int)n));
-    L.f1 = b; b += al(n * kIP * 2);
+    const int64_t N = R * n;
+    // head-major operands [R, 16, n, 128] plus one 128-row tile of slack:
+    // the flash kernel reads whole 128-row query / key tiles
+    const int64_t hm = (R * kNH * n + 128) * kDP * 2;
+    L.tmp = b; b += al(N * kH * 2);
+    L.h = b; b += al(N * kH * 2);
+    L.ar = b; b += al(N * kH * 2);
+    L.ln = b; b += al(N * kH * 2);
+    L.qkv = b; b += al(N * (kQKV > kNH * kDP ? kQKV : kNH * kDP) * 2);
+    L.q = b; b += al(hm);
+    L.k = b; b += al(hm);
+    L.v = b; b += al(hm);
+    L.vt = b; b += al(hd_flash_vt_bytes((int)R, kNH, (int)n));
+    L.f1 = b; b += al(N * kIP * 2);
     L.w2 = b; b += al((int64_t)kH * kIP * 2);
     L.cs = b; b += al(n * kD * 4);
     L.sn = b; b += al(n * kD * 4);
@@ -444,7 +450,7 @@ extern "C" void hd_vision_pos_interp(const void *pos_embed, const int *idx, cons
         return;
     }
     v_embed_kernel<<<hd_cdiv((size_t)n * (hidden / 8), 256), 256, 0, hd_stream()>>>(
-        nullptr, (const uint16_t *)pos_embed, idx, wgt, (uint16_t *)y, nullptr, n, hidden);
+        nullptr, (const uint16_t *)pos_embed, idx, wgt, (uint16_t *)y, nullptr, n, n, hidden);
     hd_check_launch("vision_pos_interp");
 }
 
@@ -543,7 +549,7 @@ extern "C" void hd_vision_deepstack_inject_n(const void *in, const uint8_t *mask
 extern "C" void hd_vision_layout(int64_t n, int64_t m, hd_vision_offsets *o) {
     (void)m;
     if (!o) return;
-    const Layout L = layout_of(n);
+    const Layout L = layout_of(1, n);
     for (int64_t *p = &o->patch_out; p <= &o->total_bytes; p++) *p = L.total;   // absent: empty
     o->patch_out = L.tmp;
     o->h_a = L.h;
@@ -563,7 +569,12 @@ extern "C" void hd_vision_layout(int64_t n, int64_t m, hd_vision_offsets *o) {
 
 extern "C" int64_t hd_vision_workspace_bytes(int64_t n) {
     if (n <= 0) return 0;
-    return layout_of(n).total;
+    return layout_of(1, n).total;
+}
+
+extern "C" int64_t hd_vision_workspace_bytes_multi(int images, int64_t n) {
+    if (n <= 0 || images <= 0) return 0;
+    return layout_of(images, n).total;
 }
 
 extern "C" int64_t hd_vision_tables_bytes(int64_t n) {
@@ -677,11 +688,14 @@ extern "C" hd_status hd_vision_prepare_tables(hd_vision_workspace *ws, int n, in
     return HD_OK;
 }
 
-extern "C" hd_status hd_vision_forward(const hd_vision_binding *bw, hd_vision_workspace *ws,
-                                       const void *pixel_values, int n, int grid_h, int grid_w,
-                                       void *image_embeds_out, void *deepstack_out[HD_VISION_NUM_DS]) {
-    if (!bw || !ws || !pixel_values || n <= 0 || grid_h <= 0 || grid_w <= 0 || !image_embeds_out ||
-        !ws->patch_out) {
+// R images of the same grid_h x grid_w: every GEMM, LayerNorm and
+// elementwise kernel runs over the R*n rows at once, attention per image
+// (the flash kernel's batch dimension).
+static hd_status forward_impl(const hd_vision_binding *bw, hd_vision_workspace *ws,
+                              const void *pixel_values, int R, int n, int grid_h, int grid_w,
+                              void *image_embeds_out, void *const *deepstack_out) {
+    if (!bw || !ws || !pixel_values || R <= 0 || n <= 0 || grid_h <= 0 || grid_w <= 0 ||
+        !image_embeds_out || !ws->patch_out) {
         hd_set_error("vision: null argument");
         return HD_ERR_MISSING;
     }
@@ -694,9 +708,9 @@ extern "C" hd_status hd_vision_forward(const hd_vision_binding *bw, hd_vision_wo
         return HD_ERR_MISSING;
     }
     hd_cuda_clear_error();
-    const int m = n / kU;
+    const int m = R * (n / kU), N = R * n;
     const float eps = 1e-6f, scale = (float)(1.0 / sqrt((double)kD));
-    const Layout L = layout_of(n);
+    const Layout L = layout_of(R, n);
     uint8_t *base = (uint8_t *)ws->patch_out;
     uint16_t *tmp = (uint16_t *)(base + L.tmp), *h = (uint16_t *)(base + L.h);
     uint16_t *ar = (uint16_t *)(base + L.ar), *ln = (uint16_t *)(base + L.ln);
@@ -706,19 +720,19 @@ extern "C" hd_status hd_vision_forward(const hd_vision_binding *bw, hd_vision_wo
     uint16_t *w2 = (uint16_t *)(base + L.w2);
     float *cs = (float *)(base + L.cs), *sn = (float *)(base + L.sn);
     hipStream_t st = hd_stream();
-    const size_t nH = (size_t)n * kH * 2;
+    const size_t nH = (size_t)N * kH * 2;
     hd_status s;
 
     // patch embed + position embedding, rotary tables
-    hd_linear(pixel_values, bw->patch_proj_w, bw->patch_proj_b, tmp, n, kH, HD_VISION_PATCH_DIM, 1);
-    v_embed_kernel<<<hd_cdiv((size_t)n * (kH / 8), 256), 256, 0, st>>>(
+    hd_linear(pixel_values, bw->patch_proj_w, bw->patch_proj_b, tmp, N, kH, HD_VISION_PATCH_DIM, 1);
+    v_embed_kernel<<<hd_cdiv((size_t)N * (kH / 8), 256), 256, 0, st>>>(
         tmp, (const uint16_t *)bw->pos_embed, (const int *)ws->pos_idx, (const float *)ws->pos_wgt,
-        nullptr, h, n, kH);
+        nullptr, h, N, n, kH);
     v_rot_kernel<<<hd_cdiv((size_t)n * (kD / 2), 256), 256, 0, st>>>(
         (const float *)ws->rot_inv, (const int *)ws->rot_coords, nullptr, cs, sn, n, kD / 4);
     if ((s = launch_err("embedding")) != HD_OK) return s;
 
-    layernorm(h, nullptr, nullptr, bw->blocks[0].norm1_w, bw->blocks[0].norm1_b, ln, n, kH, eps);
+    layernorm(h, nullptr, nullptr, bw->blocks[0].norm1_w, bw->blocks[0].norm1_b, ln, N, kH, eps);
     int ds_j = 0;
     for (int i = 0; i < HD_VISION_DEPTH; i++) {
         const hd_vision_block_binding *b = &bw->blocks[i];
@@ -727,44 +741,45 @@ extern "C" hd_status hd_vision_forward(const hd_vision_binding *bw, hd_vision_wo
             snap(s0[HD_B0_INPUT], h, nH);
             snap(s0[HD_B0_NORM1], ln, nH);
         }
-        hd_linear(ln, b->qkv_w, b->qkv_b, qkv, n, kQKV, kH, 1);
-        if (s0) snap(s0[HD_B0_QKV], qkv, (size_t)n * kQKV * 2);
-        v_qkv_rope_pad_kernel<<<hd_cdiv((size_t)kNH * n * kDP, 256), 256, 0, st>>>(
-            qkv, cs, sn, q, k, v, n, kNH, kD, kDP);
+        hd_linear(ln, b->qkv_w, b->qkv_b, qkv, N, kQKV, kH, 1);
+        if (s0) snap(s0[HD_B0_QKV], qkv, (size_t)N * kQKV * 2);
+        v_qkv_rope_pad_kernel<<<hd_cdiv((size_t)R * kNH * n * kDP, 256), 256, 0, st>>>(
+            qkv, cs, sn, q, k, v, R, n, kNH, kD, kDP);
         if (s0) {
-            snap(s0[HD_B0_Q], q, (size_t)kNH * n * kDP * 2);
-            snap(s0[HD_B0_K], k, (size_t)kNH * n * kDP * 2);
-            snap(s0[HD_B0_V], v, (size_t)kNH * n * kDP * 2);
+            snap(s0[HD_B0_Q], q, (size_t)R * kNH * n * kDP * 2);
+            snap(s0[HD_B0_K], k, (size_t)R * kNH * n * kDP * 2);
+            snap(s0[HD_B0_V], v, (size_t)R * kNH * n * kDP * 2);
         }
-        hd_flash_make_vt(v, vt, kNH, n);
-        // full attention over the zero-padded heads; output [n, 16*128] into qkv
-        if (hd_flash_attention(q, k, vt, nullptr, qkv, 1, kNH, kNH, n, kDP, 0, scale, 1)) {
+        hd_flash_make_vt(v, vt, R * kNH, n);
+        // full attention per image over the zero-padded heads; output
+        // [R*n, 16*128] (seq-major) into qkv
+        if (hd_flash_attention(q, k, vt, nullptr, qkv, R, kNH, kNH, n, kDP, 0, scale, 1)) {
             hd_set_error("vision: attention failed: %s", hd_cuda_last_error());
             return HD_ERR_RUNTIME;
         }
-        v_unpad_heads_kernel<<<hd_cdiv((size_t)n * kH, 256), 256, 0, st>>>(qkv, ln, n, kNH, kD, kDP);
+        v_unpad_heads_kernel<<<hd_cdiv((size_t)N * kH, 256), 256, 0, st>>>(qkv, ln, N, kNH, kD, kDP);
         if (s0) snap(s0[HD_B0_ATTN_MERGED], ln, nH);
-        hd_linear(ln, b->proj_w, b->proj_b, tmp, n, kH, kH, 1);
+        hd_linear(ln, b->proj_w, b->proj_b, tmp, N, kH, kH, 1);
         if (s0) snap(s0[HD_B0_PROJ], tmp, nH);
         // attn_resid = bf16(h + proj); ln = LayerNorm2(attn_resid)
-        layernorm(h, tmp, ar, b->norm2_w, b->norm2_b, ln, n, kH, eps);
+        layernorm(h, tmp, ar, b->norm2_w, b->norm2_b, ln, N, kH, eps);
         if (s0) {
             snap(s0[HD_B0_ATTN_RESID], ar, nH);
             snap(s0[HD_B0_NORM2], ln, nH);
         }
-        hd_linear_ld(ln, b->fc1_w, b->fc1_b, f1, n, kI, kH, kIP);
-        gelu_padded<true>(f1, n, kI, kIP);
-        if (s0) snap(s0[HD_B0_FC1], f1, (size_t)n * kIP * 2);
+        hd_linear_ld(ln, b->fc1_w, b->fc1_b, f1, N, kI, kH, kIP);
+        gelu_padded<true>(f1, N, kI, kIP);
+        if (s0) snap(s0[HD_B0_FC1], f1, (size_t)N * kIP * 2);
         v_pad_rows_kernel<<<hd_cdiv((size_t)kH * (kIP / 8), 256), 256, 0, st>>>(
             (const uint16_t *)b->fc2_w, w2, kH, kI, kIP);
-        hd_linear(f1, w2, b->fc2_b, tmp, n, kH, kIP, 1);
+        hd_linear(f1, w2, b->fc2_b, tmp, N, kH, kIP, 1);
         if (s0) snap(s0[HD_B0_FC2], tmp, nH);
         // h = bf16(attn_resid + fc2), then the next LayerNorm (next block's
         // norm1, or the final merger's norm over 1152)
         const bool last = i + 1 == HD_VISION_DEPTH;
         const void *nw = last ? bw->merger.norm_w : bw->blocks[i + 1].norm1_w;
         const void *nb = last ? bw->merger.norm_b : bw->blocks[i + 1].norm1_b;
-        layernorm(ar, tmp, h, nw, nb, ln, n, kH, eps);
+        layernorm(ar, tmp, h, nw, nb, ln, N, kH, eps);
         if (s0) snap(s0[HD_B0_OUTPUT], h, nH);
         if (i == 0) snap(ws->block0_snap, h, nH);
         snap(ws->block_out_snaps[i], h, nH);
@@ -775,7 +790,7 @@ extern "C" hd_status hd_vision_forward(const hd_vision_binding *bw, hd_vision_wo
             // deepstack merger: LayerNorm over 4 rows viewed as one 4608 row
             const hd_vision_merger_binding *d = &bw->deepstack[ds_j];
             void **sd = ws->ds_merger_snaps[ds_j];
-            uint16_t *dn = ar;                 // [m, 4608] == [n, 1152]; attn_resid is dead here
+            uint16_t *dn = ar;                 // [m, 4608] == [N, 1152]; attn_resid is dead here
             layernorm(h, nullptr, nullptr, d->norm_w, d->norm_b, dn, m, kU * kH, eps);
             snap(sd[0], dn, nH);
             hd_linear(dn, d->fc1_w, d->fc1_b, f1, m, kU * kH, kU * kH, 1);
@@ -800,4 +815,18 @@ extern "C" hd_status hd_vision_forward(const hd_vision_binding *bw, hd_vision_wo
     hd_linear(f1, bw->merger.fc2_w, bw->merger.fc2_b, image_embeds_out, m, kO, kU * kH, 1);
     snap(sm[4], image_embeds_out, (size_t)m * kO * 2);
     return launch_err("merger");
+}
+
+extern "C" hd_status hd_vision_forward(const hd_vision_binding *bw, hd_vision_workspace *ws,
+                                       const void *pixel_values, int n, int grid_h, int grid_w,
+                                       void *image_embeds_out, void *deepstack_out[HD_VISION_NUM_DS]) {
+    return forward_impl(bw, ws, pixel_values, 1, n, grid_h, grid_w, image_embeds_out, deepstack_out);
+}
+
+extern "C" hd_status hd_vision_forward_multi(const hd_vision_binding *bw, hd_vision_workspace *ws,
+                                             const void *pixel_values, int images, int n, int grid_h,
+                                             int grid_w, void *image_embeds_out,
+                                             void *deepstack_out[HD_VISION_NUM_DS]) {
+    return forward_impl(bw, ws, pixel_values, images, n, grid_h, grid_w, image_embeds_out,
+                        deepstack_out);
 }

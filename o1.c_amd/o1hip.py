@@ -331,6 +331,9 @@ SIGNATURES = {
     "hd_vision_prepare_tables": (c_int, [ctypes.POINTER(hd_vision_workspace), c_int, c_int, c_int]),
     "hd_vision_forward": (c_int, [ctypes.POINTER(hd_vision_binding), ctypes.POINTER(hd_vision_workspace),
                                   P, c_int, c_int, c_int, P, ctypes.POINTER(P)]),
+    "hd_vision_forward_multi": (c_int, [ctypes.POINTER(hd_vision_binding), ctypes.POINTER(hd_vision_workspace),
+                                        P, c_int, c_int, c_int, c_int, P, ctypes.POINTER(P)]),
+    "hd_vision_workspace_bytes_multi": (ctypes.c_int64, [c_int, ctypes.c_int64]),
     "hd_vision_patch": (None, [P, P, P, P, c_int, c_int, c_int]),
     "hd_vision_layernorm": (None, [P, P, P, P, c_int, c_int, c_float]),
     "hd_vision_gelu": (None, [P, P, c_size_t]),

@@ -242,6 +242,41 @@ def test_vision_tower_vs_oracle(pkg, lib, dev, vision_weights, grid):
     assert torch.equal(emb, emb2)
 
 
+def test_vision_multi_matches_single(pkg, lib, dev, vision_weights):
+    """hd_vision_forward_multi over 3 images equals 3 hd_vision_forward calls
+    row for row (per-row GEMM, per-image attention: same arithmetic)."""
+    gh, gw, R = 6, 10, 3
+    n, m = gh * gw, gh * gw // 4
+    vb = vision_binding(pkg, vision_weights)
+    tab = torch.empty(lib.hd_vision_tables_bytes(n), dtype=torch.uint8, device=dev)
+    bufs, wss = [], []
+    for imgs in (1, R):
+        ws = pkg.hd_vision_workspace()
+        buf = torch.empty(lib.hd_vision_workspace_bytes_multi(imgs, n), dtype=torch.uint8, device=dev)
+        ws.patch_out, ws.tables, ws.tables_n = buf.data_ptr(), tab.data_ptr(), -1
+        pkg.check_status(lib.hd_vision_prepare_tables(ctypes.byref(ws), n, gh, gw), "tables")
+        bufs.append(buf)
+        wss.append(ws)
+    assert lib.hd_vision_workspace_bytes_multi(1, n) == lib.hd_vision_workspace_bytes(n)
+    px = bf16(torch.randn(R * n, 1536, device=dev, generator=torch.Generator(device=dev).manual_seed(8)))
+    emb = torch.empty(R * m, OUT, dtype=torch.bfloat16, device=dev)
+    ds = [torch.empty(R * m, OUT, dtype=torch.bfloat16, device=dev) for _ in range(3)]
+    dsp = (ctypes.c_void_p * 3)(*[d.data_ptr() for d in ds])
+    pkg.check_status(lib.hd_vision_forward_multi(ctypes.byref(vb), ctypes.byref(wss[1]), pkg.ptr(px), R,
+                                                 n, gh, gw, pkg.ptr(emb), dsp), "multi")
+    for r in range(R):
+        e1 = torch.empty(m, OUT, dtype=torch.bfloat16, device=dev)
+        d1 = [torch.empty(m, OUT, dtype=torch.bfloat16, device=dev) for _ in range(3)]
+        p1 = (ctypes.c_void_p * 3)(*[d.data_ptr() for d in d1])
+        pkg.check_status(lib.hd_vision_forward(ctypes.byref(vb), ctypes.byref(wss[0]),
+                                               px[r * n:].data_ptr(), n, gh, gw, pkg.ptr(e1), p1),
+                         "single")
+        torch.cuda.synchronize()
+        assert torch.equal(e1, emb[r * m:(r + 1) * m]), r
+        for j in range(3):
+            assert torch.equal(d1[j], ds[j][r * m:(r + 1) * m]), (r, j)
+
+
 def test_forward_with_visual_vs_oracle(pkg, lib, dev):
     from tests.test_gpu_forward import TMS, grid_pos, make_forward_weights, store_names
     nL, HID, Hq, KV, FF, Dh = 4, 512, 4, 2, 1024, 128
