@@ -57,6 +57,21 @@ void hd_gemm_set_prod_backend(int backend);
 void hd_linear_ld(const void *x_dev, const void *w_dev, const void *bias_dev, void *y_dev, int M,
                   int N, int K, int ldc);
 
+/* Extension: hd_linear / hd_linear_residual with a device workspace for the
+ * tail split: when the tiles leave a last round of resident blocks at most
+ * half full, those tiles run as 2-8 K chunks writing fp32 partial tiles into
+ * ws and a merge kernel sums them (chunk order) and applies the epilogue.
+ * Results agree with the unsplit GEMM to the fp32 reassociation of the K
+ * sum (then one bf16 rounding). ws 16-byte aligned; ws == NULL or too small
+ * runs the unsplit GEMM. Launches on one stream must not share ws
+ * concurrently. */
+void hd_linear_ws(const void *x_dev, const void *w_dev, const void *bias_dev, void *y_dev, int M,
+                  int N, int K, void *ws, int64_t ws_bytes);
+void hd_linear_residual_ws(const void *x_dev, const void *w_dev, const void *res_dev, void *y_dev,
+                           int M, int N, int K, void *ws, int64_t ws_bytes);
+/* Workspace bytes that let every tail split of the current device run. */
+int64_t hd_gemm_ws_bytes(void);
+
 /* ---- fused-epilogue entry points (extension) --------------------------
  * y = bf16(res + bf16(x . W^T))      : residual epilogue (o_proj, down)   */
 void hd_linear_residual(const void *x_dev, const void *w_dev,

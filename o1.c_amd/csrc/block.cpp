@@ -58,8 +58,10 @@ static BlockScratch carve(void *base, int batch, int64_t seq, int heads, int kv,
     s.ar = take(M * hidden * 2);
     s.swi = take(M * (int64_t)ff * 2);
     s.cs = with_cs ? (float *)take(seq * (int64_t)hd * 4) : nullptr;   // [seq, hd/2] x (cos,sin)
-    s.fa_ws_bytes = hd_flash_ws_bytes();
-    s.fa_ws = take(s.fa_ws_bytes);                                      // attention tail split
+    // tail splits of attention and of the o_proj / down GEMMs share one
+    // region (they run one after the other on the stream)
+    s.fa_ws_bytes = hd_flash_ws_bytes() > hd_gemm_ws_bytes() ? hd_flash_ws_bytes() : hd_gemm_ws_bytes();
+    s.fa_ws = take(s.fa_ws_bytes);
     s.bytes = o;
     return s;
 }
@@ -160,7 +162,7 @@ static hd_status block_core(const void *in, const float *cs, const void *mask, i
     if (hd_flash_attention_ws(s.q, s.k, s.vt, mask, s.attn, batch, H, KV, (int)seq, D, ar_len,
                               scale, 1, s.fa_ws, s.fa_ws_bytes) != 0)
         return launch_status("attention");
-    hd_linear_residual(s.attn, bw->o_proj, in, s.ar, M, HID, H * D);
+    hd_linear_residual_ws(s.attn, bw->o_proj, in, s.ar, M, HID, H * D, s.fa_ws, s.fa_ws_bytes);
     if (ints && ints->attn_hidden) hd_linear(s.attn, bw->o_proj, nullptr, ints->attn_hidden, M, HID, H * D, 1);
     if (ints && ints->attn_resid) {
         hd_status st = copy_d2d(ints->attn_resid, s.ar, (size_t)M * HID * 2);
@@ -173,7 +175,7 @@ static hd_status block_core(const void *in, const float *cs, const void *mask, i
     }
     hd_linear_swiglu(s.ln, bw->gate_proj, bw->up_proj, s.swi, M, FF, HID);
     if (ints && ints->mlp_out) hd_linear(s.swi, bw->down_proj, nullptr, ints->mlp_out, M, HID, FF, 1);
-    hd_linear_residual(s.swi, bw->down_proj, s.ar, out, M, HID, FF);
+    hd_linear_residual_ws(s.swi, bw->down_proj, s.ar, out, M, HID, FF, s.fa_ws, s.fa_ws_bytes);
     return launch_status("launch");
 }
 

@@ -45,6 +45,11 @@ struct GemmArgs {
     uint16_t *q_out, *k_out, *vt_out;
     int seq, heads, kv_heads;
     float eps;
+    // tail split (gemm_ms_kernel): blocks < n_whole run whole tiles; the
+    // blocks after them run the K chunks (split per tile) of the last
+    // n_tail tiles and write fp32 partial tiles [BM][BN] to `part`
+    int n_whole, split;
+    float *part;
 };
 
 __device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
@@ -449,14 +454,29 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
-    const int nblk = g.ntm * g.ntn;
-    const int lin = xcd_remap(blockIdx.x, nblk);
+    // whole tiles first (XCD-contiguous over them), then the K chunks of the
+    // tail tiles (lin >= n_whole), `split` consecutive blocks per tile
+    int lin, chunk = -1, item = 0;
+    if ((int)blockIdx.x < g.n_whole) {
+        lin = xcd_remap(blockIdx.x, g.n_whole);
+    } else {
+        item = blockIdx.x - g.n_whole;
+        chunk = item % g.split;
+        lin = g.n_whole + item / g.split;
+    }
     const int in_group = GROUP_M * g.ntn;
     const int first_m = (lin / in_group) * GROUP_M;
     const int gm = min(g.ntm - first_m, GROUP_M);
     const int tm = first_m + (lin % in_group) % gm;
     const int tn = (lin % in_group) / gm;
     const int m0 = tm * BM;
+    // K tiles of this block: all, or chunk `chunk` of `split`
+    int kbase = 0, nk = g.K / BK;
+    if (chunk >= 0) {
+        const int k0 = chunk * nk / g.split, k1 = (chunk + 1) * nk / g.split;
+        kbase = k0;
+        nk = k1 - k0;
+    }
 
     const uint16_t *a_src[AI];
     const uint16_t *b_src[BI];
@@ -490,7 +510,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
     }
     // LDR 2 (diagnostic): every K tile re-reads tile 0, so all loads hit in
     // cache and the instruction stream is otherwise unchanged
-    auto koff = [&](int kt) { return LDR == 2 ? 0 : kt * BK; };
+    auto koff = [&](int kt) { return LDR == 2 ? 0 : (kbase + kt) * BK; };
     // LDR 5: buffer loads straight to LDS (MUBUF: 32-bit per-lane byte
     // offsets against a scalar descriptor; the K advance is the scalar
     // offset; rows past the matrix read as zero through the record limit)
@@ -532,7 +552,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
         if (LDR == 3) return;   // diagnostic: no global->LDS traffic
         uint16_t *As = smem + st * C::STAGE, *Bs = As + BM * BK;
         if constexpr (LDR == 5) {
-            const uint32_t so = (uint32_t)kt * BK * 2;
+            const uint32_t so = (uint32_t)(kbase + kt) * BK * 2;
 #pragma unroll
             for (int i = 0; i < AI; i++)
                 buf_load_lds16(bp_a, nb_a, a_vo[i], so, (HD_LDS void *)(As + (wave * AI + i) * 512));
@@ -556,9 +576,9 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
     u32x4_t ra[AI], rb[BI];
     auto gload = [&](int kt) {
 #pragma unroll
-        for (int i = 0; i < AI; i++) ra[i] = *(const u32x4_t *)(a_src[i] + kt * BK);
+        for (int i = 0; i < AI; i++) ra[i] = *(const u32x4_t *)(a_src[i] + (kbase + kt) * BK);
 #pragma unroll
-        for (int i = 0; i < BI; i++) rb[i] = *(const u32x4_t *)(b_src[i] + kt * BK);
+        for (int i = 0; i < BI; i++) rb[i] = *(const u32x4_t *)(b_src[i] + (kbase + kt) * BK);
     };
     auto lstore = [&](int st) {
         uint16_t *As = smem + st * C::STAGE, *Bs = As + BM * BK;
@@ -576,7 +596,6 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
 #pragma unroll
             for (int r = 0; r < ACCN; r++) acc[i][j][r] = 0.f;
 
-    const int nk = g.K / BK;
     const int l32 = lane & 31, khalf = lane >> 5;
     const int sw = ms_swz<CPR>(l32);
     if constexpr (SGB == 3) {
@@ -737,6 +756,27 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
             __syncthreads();
         }
     }
+    }
+    if constexpr (MF == 32 && EPI != EPI_QKV) {
+        if (chunk >= 0) {
+            // K chunk of a tail tile: the raw fp32 accumulators, tile-local
+            // [BM][BN] in accumulator column order; the merge kernel sums
+            // the chunks and applies the epilogue
+            float *pt = g.part + (size_t)item * BM * BN;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int row = wm * WTM + i * 32 + l32;
+                        const int col = wn * WTN + j * 32 + q * 8 + khalf * 4;
+                        f32x4_t v = {acc[i][j][q * 4], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2],
+                                     acc[i][j][q * 4 + 3]};
+                        *(f32x4_t *)(pt + (size_t)row * BN + col) = v;
+                    }
+            return;
+        }
     }
     __syncthreads();   // every wave is done with the ring before staging reuses it
 
@@ -1062,14 +1102,102 @@ static void launch_cfg(GemmArgs &g) {
         <<<g.ntm * g.ntn, Cfg::NT, 0, hd_stream()>>>(g);
 }
 
+// Sums the K chunks of each tail tile (fp32, chunk order) and applies the
+// epilogue exactly as gemm_ms_kernel does on its accumulators: four output
+// columns per thread.
+template <int BM, int BN, int WGN, int EPI>
+__global__ void gemm_tail_merge_kernel(GemmArgs g, int n_tail) {
+    constexpr int BN_OUT = EPI == EPI_SWIGLU ? BN / 2 : BN, WTN = BN / WGN, WO = EPI == EPI_SWIGLU ? WTN / 2 : WTN;
+    constexpr int GROUP_M = 8;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)n_tail * BM * (BN_OUT / 4)) return;
+    const int c = (int)(i % (BN_OUT / 4)) * 4, r = (int)((i / (BN_OUT / 4)) % BM);
+    const int t = (int)(i / ((size_t)BM * (BN_OUT / 4)));
+    const int lin = g.n_whole + t;
+    const int in_group = GROUP_M * g.ntn;
+    const int first_m = (lin / in_group) * GROUP_M;
+    const int gm = min(g.ntm - first_m, GROUP_M);
+    const int tm = first_m + (lin % in_group) % gm, tn = (lin % in_group) / gm;
+    const int m = tm * BM + r, n = tn * BN_OUT + c;
+    if (m >= g.M || n >= g.N) return;
+    const int ca = EPI == EPI_SWIGLU ? (c / WO) * WTN + c % WO : c;   // accumulator column
+    f32x4_t a = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+    for (int p = 0; p < g.split; p++) {
+        const float *pt = g.part + ((size_t)(t * g.split + p) * BM + r) * BN;
+        a += *(const f32x4_t *)(pt + ca);
+        if (EPI == EPI_SWIGLU) u += *(const f32x4_t *)(pt + ca + WTN / 2);
+    }
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        float x = a[e];
+        if (EPI == EPI_SWIGLU) {
+            const float gt = bfround(x), up = bfround(u[e]);
+            const float sg = bfround(gt * (1.0f / (1.0f + __expf(-gt))));
+            x = sg * up;
+        }
+        v[e] = x;
+    }
+    u32x2_t pk = {pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+    if (EPI == EPI_BIAS || EPI == EPI_RES) {
+        const uint16_t *o = EPI == EPI_BIAS ? g.bias + n : g.res + (size_t)m * g.ldc + n;
+        const u32x2_t ov = *(const u32x2_t *)o;
+#pragma unroll
+        for (int e = 0; e < 2; e++) pk[e] = pack_bf2(lo_bf(pk[e]) + lo_bf(ov[e]), hi_bf(pk[e]) + hi_bf(ov[e]));
+    }
+    *(u32x2_t *)(g.C + (size_t)m * g.ldc + n) = pk;
+}
+
+// Resident blocks of one round (one GEMM block per CU).
+static int gemm_slots() {
+    static int dev_cached = -1, cus = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (dev != dev_cached) {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 0;
+        dev_cached = dev;
+    }
+    return cus;
+}
+
+// Tail split plan for `units` tiles of nk K tiles: the tiles of the last,
+// partly filled round run as P K chunks (2..8) when that round is at most
+// half full and the partial tiles fit in ws_bytes. Returns P (1: no split).
+static int tail_split_of(long units, int nk, size_t tile_bytes, int64_t ws_bytes) {
+    const int slots = gemm_slots();
+    if (slots <= 0 || ws_bytes <= 0) return 1;
+    const long rem = units % slots;
+    if (rem == 0 || rem > slots / 2) return 1;
+    int P = (int)(slots / rem);
+    if (P > 8) P = 8;
+    if (P > nk / 4) P = nk / 4;   // chunks of at least 4 K tiles
+    if (P < 2 || (int64_t)rem * P * (int64_t)tile_bytes > ws_bytes) return 1;
+    return P;
+}
+
 template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 0, int OCC = 1,
           int LDR = 0, int MF = 32>
-static void launch_ms(GemmArgs &g) {
+static void launch_ms(GemmArgs &g, void *ws = nullptr, int64_t ws_bytes = 0) {
     using Cfg = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI, MF>;
     g.ntm = (g.M + BM - 1) / BM;
     g.ntn = (g.N + Cfg::BN_OUT - 1) / Cfg::BN_OUT;
+    const long units = (long)g.ntm * g.ntn;
+    int P = 1;
+    if (ws && EPI != EPI_QKV && MF == 32 && OCC == 1)
+        P = tail_split_of(units, g.K / BK, (size_t)BM * BN * 4, ws_bytes);
+    const long n_tail = P > 1 ? units % gemm_slots() : 0;
+    g.n_whole = (int)(units - n_tail);
+    g.split = P;
+    g.part = (float *)ws;
     gemm_ms_kernel<BM, BN, BK, NS, WGM, WGN, EPI, SGB, OCC, LDR, MF>
-        <<<g.ntm * g.ntn, Cfg::NT, 0, hd_stream()>>>(g);
+        <<<(unsigned)(g.n_whole + n_tail * P), Cfg::NT, 0, hd_stream()>>>(g);
+    if (n_tail) {
+        if constexpr (EPI != EPI_QKV)
+            gemm_tail_merge_kernel<BM, BN, WGN, EPI>
+                <<<hd_cdiv((size_t)n_tail * BM * (Cfg::BN_OUT / 4), 256), 256, 0, hd_stream()>>>(
+                    g, (int)n_tail);
+    }
 }
 
 template <int BM, int EPI>
@@ -1150,7 +1278,7 @@ static double quant_eff(long tiles) {
 }
 
 template <int EPI>
-static const char *pick_and_launch(GemmArgs &g, bool launch) {
+static const char *pick_and_launch(GemmArgs &g, bool launch, void *ws = nullptr, int64_t ws_bytes = 0) {
     const int bn_out = EPI == EPI_SWIGLU ? 128 : 256;
     const long tn = (g.N + bn_out - 1) / bn_out;
     const long t256 = (long)((g.M + 255) / 256) * tn;
@@ -1159,41 +1287,53 @@ static const char *pick_and_launch(GemmArgs &g, bool launch) {
         if (launch) launch_ms<128, 128, 64, 2, 2, 2, EPI, 1, 2>(g);
         return "bf16_128x128x64_w2x2_occ2";
     }
-    // 192-row tiles compute 25% fewer rows per tile for the same overheads;
-    // take them only when the quantisation gain outweighs that (~12%).
-    // K <= 8192: 4 waves of 128x128 with one fragment ring across the K loop,
-    // operands through buffer loads straight to LDS (byte offsets must stay
-    // below 2^31: each operand under 2 GiB); the deep-K (down projection)
-    // shapes run faster on 8 interleaved waves.
+    // K <= 8192: 4 waves of 128x128 with one fragment ring across the K loop;
+    // deeper K: 8 interleaved waves. Operands through buffer loads straight
+    // to LDS when each is under 2 GiB (32-bit byte offsets).
     const bool fits = (size_t)(g.M + 256) * g.K * 2 < ((size_t)1 << 31) &&
                       (size_t)g.N * g.K * 2 < ((size_t)1 << 31);
     const bool ring = g_family == 0 && g.K <= 8192 && fits;
-    if (quant_eff(t192) > quant_eff(t256) * 1.12) {
+    // With a workspace, a last round that is at most half full runs as K
+    // chunks of its tiles (tail split): 256-row tiles then keep their
+    // per-flop efficiency (192-row tiles are 8-18 % slower per flop) at the
+    // quantisation cost of a fraction of a round.
+    const bool split256 = ws && tail_split_of(t256, g.K / 64, (size_t)256 * 256 * 4, ws_bytes) > 1;
+    // otherwise 192-row tiles when they quantise the grid enough better
+    const bool use192 = !split256 && quant_eff(t192) > quant_eff(t256) * 1.12;
+    if (use192) {
         if (ring) {
-            if (launch) launch_ms<192, 256, 64, 2, 2, 2, EPI, 3, 1, 5>(g);
+            if (launch) launch_ms<192, 256, 64, 2, 2, 2, EPI, 3, 1, 5>(g, ws, ws_bytes);
             return "bf16_192x256x64_w2x2_ring_buf";
         }
-        if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 1>(g);
+        if (fits && g_family == 0) {
+            if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 1, 1, 5>(g, ws, ws_bytes);
+            return "bf16_192x256x64_w2x4_ilv_buf";
+        }
+        if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 1>(g, ws, ws_bytes);
         return "bf16_192x256x64_w2x4_ilv";
     }
     if (ring) {
-        if (launch) launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 5>(g);
-        return "bf16_256x256x64_w2x2_ring_buf";
+        if (launch) launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 5>(g, ws, ws_bytes);
+        return split256 ? "bf16_256x256x64_w2x2_ring_buf_tailsplit" : "bf16_256x256x64_w2x2_ring_buf";
     }
-    if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 1>(g);
-    return "bf16_256x256x64_w2x4_ilv";
+    if (fits && g_family == 0) {
+        if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 1, 1, 5>(g, ws, ws_bytes);
+        return split256 ? "bf16_256x256x64_w2x4_ilv_buf_tailsplit" : "bf16_256x256x64_w2x4_ilv_buf";
+    }
+    if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 1>(g, ws, ws_bytes);
+    return split256 ? "bf16_256x256x64_w2x4_ilv_tailsplit" : "bf16_256x256x64_w2x4_ilv";
 }
 
 static bool mfma_ok(const void *x, const void *y, int N, int K) {
     return K % 64 == 0 && N % 8 == 0 && ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0);
 }
 
-static void gemm_launch(int epi, GemmArgs &g) {
+static void gemm_launch(int epi, GemmArgs &g, void *ws = nullptr, int64_t ws_bytes = 0) {
     switch (epi) {
-    case EPI_NONE: pick_and_launch<EPI_NONE>(g, true); break;
-    case EPI_BIAS: pick_and_launch<EPI_BIAS>(g, true); break;
-    case EPI_RES: pick_and_launch<EPI_RES>(g, true); break;
-    case EPI_SWIGLU: pick_and_launch<EPI_SWIGLU>(g, true); break;
+    case EPI_NONE: pick_and_launch<EPI_NONE>(g, true, ws, ws_bytes); break;
+    case EPI_BIAS: pick_and_launch<EPI_BIAS>(g, true, ws, ws_bytes); break;
+    case EPI_RES: pick_and_launch<EPI_RES>(g, true, ws, ws_bytes); break;
+    case EPI_SWIGLU: pick_and_launch<EPI_SWIGLU>(g, true, ws, ws_bytes); break;
     }
 }
 
@@ -1316,6 +1456,24 @@ extern "C" void hd_linear(const void *x, const void *w, const void *bias, void *
     hd_check_launch("linear");
 }
 
+extern "C" void hd_linear_ws(const void *x, const void *w, const void *bias, void *y, int M, int N,
+                             int K, void *ws, int64_t ws_bytes) {
+    if (!x || !w || !y || M <= 0 || N <= 0 || K <= 0 || !mfma_ok(x, y, N, K) ||
+        (bias && (uintptr_t)bias % 16) || (ws && (uintptr_t)ws % 16) || !g_use_production) {
+        hd_linear(x, w, bias, y, M, N, K, 1);
+        return;
+    }
+    GemmArgs g = {};
+    g.A = (const uint16_t *)x;
+    g.B[0] = g.B[1] = g.B[2] = (const uint16_t *)w;
+    g.seg_end[0] = g.seg_end[1] = g.seg_end[2] = N;
+    g.C = (uint16_t *)y;
+    g.bias = (const uint16_t *)bias;
+    g.M = M; g.N = N; g.K = K; g.ldc = N;
+    gemm_launch(bias ? EPI_BIAS : EPI_NONE, g, ws, ws ? ws_bytes : 0);
+    hd_check_launch("linear");
+}
+
 // hd_linear writing rows of stride ldc (>= N, ldc % 8 == 0): the vision
 // tower's fc1 lands in a row padded to the next GEMM's K.
 extern "C" void hd_linear_ld(const void *x, const void *w, const void *bias, void *y, int M, int N,
@@ -1336,10 +1494,10 @@ extern "C" void hd_linear_ld(const void *x, const void *w, const void *bias, voi
     hd_check_launch("linear_ld");
 }
 
-extern "C" void hd_linear_residual(const void *x, const void *w, const void *res, void *y, int M,
-                                   int N, int K) {
+extern "C" void hd_linear_residual_ws(const void *x, const void *w, const void *res, void *y, int M,
+                                      int N, int K, void *ws, int64_t ws_bytes) {
     if (!x || !w || !res || !y || M <= 0 || N <= 0 || K <= 0 || !mfma_ok(x, y, N, K) ||
-        (uintptr_t)res % 16) {
+        (uintptr_t)res % 16 || (ws && (uintptr_t)ws % 16)) {
         snprintf(hd_cuda_errbuf(), 512, "linear_residual: bad args");
         return;
     }
@@ -1350,8 +1508,20 @@ extern "C" void hd_linear_residual(const void *x, const void *w, const void *res
     g.C = (uint16_t *)y;
     g.res = (const uint16_t *)res;
     g.M = M; g.N = N; g.K = K; g.ldc = N;
-    gemm_launch(EPI_RES, g);
+    gemm_launch(EPI_RES, g, ws, ws ? ws_bytes : 0);
     hd_check_launch("linear_residual");
+}
+
+extern "C" void hd_linear_residual(const void *x, const void *w, const void *res, void *y, int M,
+                                   int N, int K) {
+    hd_linear_residual_ws(x, w, res, y, M, N, K, nullptr, 0);
+}
+
+// Workspace for the tail split of one GEMM on the current device: half a
+// round of 256x256 fp32 partial tiles, split at most 8 ways.
+extern "C" int64_t hd_gemm_ws_bytes(void) {
+    const int slots = gemm_slots();
+    return (int64_t)(slots > 0 ? slots : 256) * 256 * 256 * 4;
 }
 
 extern "C" void hd_linear_swiglu(const void *x, const void *wg, const void *wu, void *y, int M,

@@ -378,3 +378,46 @@ def test_flash_tail_split_matches_unsplit(pkg, lib, dev, S, seq_major):
     # in at least a few bits somewhere, or match exactly when the merge
     # reproduces the rounding; both are fine, but nothing may be left zero
     assert float(bf.abs().sum(dim=-1).min()) > 0
+
+
+@pytest.mark.parametrize("K", [4096, 12288])
+@pytest.mark.parametrize("bias", [False, True])
+def test_gemm_tail_split(pkg, lib, dev, K, bias):
+    """hd_linear_residual_ws / hd_linear_ws: M = 8448 gives 33 x 16 = 528
+    tiles of 256x256, two rounds of 256 CUs plus 16 tail tiles that run as
+    K chunks. Whole tiles equal the unsplit GEMM bit for bit; tail tiles
+    differ only by the fp32 reassociation of the K sum (one bf16 step)."""
+    M, N = 8448, 4096
+    print(f"tail split K={K} bias={bias}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(K + bias)
+    x = (torch.randn(M, K, device=dev, generator=g)).to(torch.bfloat16)
+    w = (torch.randn(N, K, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    r = torch.randn(M, N, device=dev, generator=g).to(torch.bfloat16)
+    b = (torch.randn(N, device=dev, generator=g) * 0.1).to(torch.bfloat16) if bias else None
+    ws = torch.empty(lib.hd_gemm_ws_bytes(), dtype=torch.uint8, device=dev)
+    y0, y1 = torch.empty(M, N, dtype=torch.bfloat16, device=dev), torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    if bias:
+        lib.hd_linear(pkg.ptr(x), pkg.ptr(w), pkg.ptr(b), pkg.ptr(y0), M, N, K, 1)
+        lib.hd_linear_ws(pkg.ptr(x), pkg.ptr(w), pkg.ptr(b), pkg.ptr(y1), M, N, K, pkg.ptr(ws), ws.numel())
+        want = ((x.float() @ w.float().t()).to(torch.bfloat16).float() + b.float())
+    else:
+        lib.hd_linear_residual(pkg.ptr(x), pkg.ptr(w), pkg.ptr(r), pkg.ptr(y0), M, N, K)
+        lib.hd_linear_residual_ws(pkg.ptr(x), pkg.ptr(w), pkg.ptr(r), pkg.ptr(y1), M, N, K,
+                                  pkg.ptr(ws), ws.numel())
+        want = (x.float() @ w.float().t()).to(torch.bfloat16).float() + r.float()
+    pkg.check_prim("tail split")
+    torch.cuda.synchronize()
+    a, c = y0.float(), y1.float()
+    diff = (a - c).abs()
+    # one bf16 step of the GEMM sum (rounded before the bias / residual add)
+    # plus one of the output
+    acc = (x.float() @ w.float().t()).abs()
+    step = (acc + a.abs()) * 2.0 ** -7 + 1e-6
+    worst = int(torch.argmax(diff - step))
+    print("worst", a.flatten()[worst].item(), c.flatten()[worst].item(), acc.flatten()[worst].item())
+    assert bool((diff <= step).all())
+    same = float((diff == 0).float().mean())
+    assert same >= 512 / 528 - 1e-3, same        # whole tiles bit-identical
+    assert same < 1.0                            # the tail did run split
+    rel = float((c - want).norm() / want.norm())
+    assert rel < 5e-3, rel
