@@ -111,6 +111,12 @@ int hd_linear_qkv_rope(const void *x, const void *wq, const void *wk, const void
                        const void *qn_w, const void *kn_w, const float *cs, void *q, void *k,
                        void *vt, int batch, int seq, int heads, int kv_heads, int hidden,
                        float eps);
+/* Extension: hd_linear_qkv_rope with the tail-split workspace of
+ * hd_linear_residual_ws (the tail tiles' epilogue runs in the merge). */
+int hd_linear_qkv_rope_ws(const void *x, const void *wq, const void *wk, const void *wv,
+                          const void *qn_w, const void *kn_w, const float *cs, void *q, void *k,
+                          void *vt, int batch, int seq, int heads, int kv_heads, int hidden,
+                          float eps, void *ws, int64_t ws_bytes);
 
 /* Diagnostics/tuning: kernel family for the production GEMMs. 0 (default):
  * 4-wave fragment-ring tiles for K <= 8192, 8-wave interleaved tiles above;

@@ -151,9 +151,9 @@ static hd_status block_core(const void *in, const float *cs, const void *mask, i
     }
     // QKV GEMM with q/k norm + rotary + V^T layout in its epilogue; shapes
     // outside that path take the GEMM then the standalone epilogue kernels
-    if (D != 128 || hd_linear_qkv_rope(s.ln, bw->q_proj, bw->k_proj, bw->v_proj, bw->q_norm,
-                                       bw->k_norm, cs, s.q, s.k, s.vt, batch, (int)seq, H, KV,
-                                       HID, eps) != 0) {
+    if (D != 128 || hd_linear_qkv_rope_ws(s.ln, bw->q_proj, bw->k_proj, bw->v_proj, bw->q_norm,
+                                          bw->k_norm, cs, s.q, s.k, s.vt, batch, (int)seq, H, KV,
+                                          HID, eps, s.fa_ws, s.fa_ws_bytes) != 0) {
         hd_linear_concat3(s.ln, bw->q_proj, H * D, bw->k_proj, KV * D, bw->v_proj, KV * D, s.qkv,
                           M, HID);
         hd_qkv_epilogue(s.qkv, bw->q_norm, bw->k_norm, cs, s.q, s.k, nullptr, s.vt, batch,

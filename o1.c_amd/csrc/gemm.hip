@@ -757,7 +757,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
         }
     }
     }
-    if constexpr (MF == 32 && EPI != EPI_QKV) {
+    if constexpr (MF == 32) {
         if (chunk >= 0) {
             // K chunk of a tail tile: the raw fp32 accumulators, tile-local
             // [BM][BN] in accumulator column order; the merge kernel sums
@@ -1121,6 +1121,9 @@ __global__ void gemm_tail_merge_kernel(GemmArgs g, int n_tail) {
     const int m = tm * BM + r, n = tn * BN_OUT + c;
     if (m >= g.M || n >= g.N) return;
     const int ca = EPI == EPI_SWIGLU ? (c / WO) * WTN + c % WO : c;   // accumulator column
+    // EPI_QKV: bf16 projection of the tail tiles into a tile-local staging
+    // area after the partials; gemm_tail_qkv_epi_kernel finishes them
+    uint16_t *const stage = EPI == EPI_QKV ? (uint16_t *)(g.part + (size_t)n_tail * g.split * BM * BN) : nullptr;
     f32x4_t a = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
     for (int p = 0; p < g.split; p++) {
         const float *pt = g.part + ((size_t)(t * g.split + p) * BM + r) * BN;
@@ -1139,6 +1142,10 @@ __global__ void gemm_tail_merge_kernel(GemmArgs g, int n_tail) {
         v[e] = x;
     }
     u32x2_t pk = {pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+    if (EPI == EPI_QKV) {
+        *(u32x2_t *)(stage + ((size_t)t * BM + r) * BN + c) = pk;
+        return;
+    }
     if (EPI == EPI_BIAS || EPI == EPI_RES) {
         const uint16_t *o = EPI == EPI_BIAS ? g.bias + n : g.res + (size_t)m * g.ldc + n;
         const u32x2_t ov = *(const u32x2_t *)o;
@@ -1146,6 +1153,34 @@ __global__ void gemm_tail_merge_kernel(GemmArgs g, int n_tail) {
         for (int e = 0; e < 2; e++) pk[e] = pack_bf2(lo_bf(pk[e]) + lo_bf(ov[e]), hi_bf(pk[e]) + hi_bf(ov[e]));
     }
     *(u32x2_t *)(g.C + (size_t)m * g.ldc + n) = pk;
+}
+
+// EPI_QKV tail tiles, second pass: one wave per (tile, 32-row slice, head)
+// copies its slice of the staged bf16 projection into LDS in the layout
+// gemm_ms_kernel stages it and runs the same qkv_epilogue.
+template <int BM, int BN>
+__global__ __launch_bounds__(64) void gemm_tail_qkv_epi_kernel(GemmArgs g, int n_tail) {
+    constexpr int RS = 32, LDW = 128 + 8, GROUP_M = 8, NSL = BM / RS, NH = BN / 128;
+    __shared__ __attribute__((aligned(16))) uint16_t stg[RS * LDW];
+    const int lane = threadIdx.x;
+    const int b = blockIdx.x;
+    const int hc = b % NH, sl = (b / NH) % NSL, t = b / (NH * NSL);
+    const int lin = g.n_whole + t;
+    const int in_group = GROUP_M * g.ntn;
+    const int first_m = (lin / in_group) * GROUP_M;
+    const int gm = min(g.ntm - first_m, GROUP_M);
+    const int tm = first_m + (lin % in_group) % gm, tn = (lin % in_group) / gm;
+    const uint16_t *src = (const uint16_t *)(g.part + (size_t)n_tail * g.split * BM * BN) +
+                          ((size_t)t * BM + sl * RS) * BN + hc * 128;
+#pragma unroll
+    for (int idx = lane; idx < RS * 16; idx += 64) {
+        const int r = idx / 16, c = (idx % 16) * 8;
+        *(u32x4_t *)(stg + r * LDW + c) = *(const u32x4_t *)(src + (size_t)r * BN + c);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    qkv_epilogue<RS, LDW>(g, stg, tm * BM + sl * RS, (tn * BN) / 128 + hc, lane);
 }
 
 // Resident blocks of one round (one GEMM block per CU).
@@ -1164,7 +1199,8 @@ static int gemm_slots() {
 // Tail split plan for `units` tiles of nk K tiles: the tiles of the last,
 // partly filled round run as P K chunks (2..8) when that round is at most
 // half full and the partial tiles fit in ws_bytes. Returns P (1: no split).
-static int tail_split_of(long units, int nk, size_t tile_bytes, int64_t ws_bytes) {
+static int tail_split_of(long units, int nk, size_t tile_bytes, int64_t ws_bytes,
+                         size_t stage_bytes = 0) {
     const int slots = gemm_slots();
     if (slots <= 0 || ws_bytes <= 0) return 1;
     const long rem = units % slots;
@@ -1172,7 +1208,7 @@ static int tail_split_of(long units, int nk, size_t tile_bytes, int64_t ws_bytes
     int P = (int)(slots / rem);
     if (P > 8) P = 8;
     if (P > nk / 4) P = nk / 4;   // chunks of at least 4 K tiles
-    if (P < 2 || (int64_t)rem * P * (int64_t)tile_bytes > ws_bytes) return 1;
+    if (P < 2 || (int64_t)rem * (P * (int64_t)tile_bytes + (int64_t)stage_bytes) > ws_bytes) return 1;
     return P;
 }
 
@@ -1184,8 +1220,9 @@ static void launch_ms(GemmArgs &g, void *ws = nullptr, int64_t ws_bytes = 0) {
     g.ntn = (g.N + Cfg::BN_OUT - 1) / Cfg::BN_OUT;
     const long units = (long)g.ntm * g.ntn;
     int P = 1;
-    if (ws && EPI != EPI_QKV && MF == 32 && OCC == 1)
-        P = tail_split_of(units, g.K / BK, (size_t)BM * BN * 4, ws_bytes);
+    if (ws && MF == 32 && OCC == 1)
+        P = tail_split_of(units, g.K / BK, (size_t)BM * BN * 4, ws_bytes,
+                          EPI == EPI_QKV ? (size_t)BM * BN * 2 : 0);
     const long n_tail = P > 1 ? units % gemm_slots() : 0;
     g.n_whole = (int)(units - n_tail);
     g.split = P;
@@ -1193,10 +1230,12 @@ static void launch_ms(GemmArgs &g, void *ws = nullptr, int64_t ws_bytes = 0) {
     gemm_ms_kernel<BM, BN, BK, NS, WGM, WGN, EPI, SGB, OCC, LDR, MF>
         <<<(unsigned)(g.n_whole + n_tail * P), Cfg::NT, 0, hd_stream()>>>(g);
     if (n_tail) {
-        if constexpr (EPI != EPI_QKV)
-            gemm_tail_merge_kernel<BM, BN, WGN, EPI>
-                <<<hd_cdiv((size_t)n_tail * BM * (Cfg::BN_OUT / 4), 256), 256, 0, hd_stream()>>>(
-                    g, (int)n_tail);
+        gemm_tail_merge_kernel<BM, BN, WGN, EPI>
+            <<<hd_cdiv((size_t)n_tail * BM * (Cfg::BN_OUT / 4), 256), 256, 0, hd_stream()>>>(
+                g, (int)n_tail);
+        if constexpr (EPI == EPI_QKV)
+            gemm_tail_qkv_epi_kernel<BM, BN>
+                <<<(unsigned)(n_tail * (BM / 32) * (BN / 128)), 64, 0, hd_stream()>>>(g, (int)n_tail);
     }
 }
 
@@ -1341,10 +1380,10 @@ static void gemm_launch(int epi, GemmArgs &g, void *ws = nullptr, int64_t ws_byt
 // the GEMM epilogue (EPI_QKV). Returns 1 without launching when the shape is
 // outside the fused path (the caller then runs hd_linear_concat3 +
 // hd_qkv_epilogue, which compute the same values).
-extern "C" int hd_linear_qkv_rope(const void *x, const void *wq, const void *wk, const void *wv,
-                                  const void *qn_w, const void *kn_w, const float *cs, void *q,
-                                  void *k, void *vt, int batch, int seq, int heads, int kv_heads,
-                                  int hidden, float eps) {
+extern "C" int hd_linear_qkv_rope_ws(const void *x, const void *wq, const void *wk, const void *wv,
+                                     const void *qn_w, const void *kn_w, const float *cs, void *q,
+                                     void *k, void *vt, int batch, int seq, int heads, int kv_heads,
+                                     int hidden, float eps, void *ws, int64_t ws_bytes) {
     if (!x || !wq || !wk || !wv || !qn_w || !kn_w || !cs || !q || !k || !vt || batch <= 0 ||
         seq <= 0 || heads <= 0 || kv_heads <= 0 || hidden <= 0)
         return 1;
@@ -1373,10 +1412,23 @@ extern "C" int hd_linear_qkv_rope(const void *x, const void *wq, const void *wk,
     g.seq = seq; g.heads = heads; g.kv_heads = kv_heads; g.eps = eps;
     const long tn = N / 256;
     const long t256 = (long)((M + 255) / 256) * tn, t192 = (long)((M + 191) / 192) * tn;
-    if (quant_eff(t192) > quant_eff(t256) * 1.12) launch_ms<192, 256, 64, 2, 2, 2, EPI_QKV, 3, 1, 5>(g);
-    else launch_ms<256, 256, 64, 2, 2, 2, EPI_QKV, 3, 1, 5>(g);
+    if (ws && (uintptr_t)ws % 16) ws = nullptr;
+    const bool split256 =
+        ws && tail_split_of(t256, hidden / 64, (size_t)256 * 256 * 4, ws_bytes, (size_t)256 * 256 * 2) > 1;
+    if (!split256 && quant_eff(t192) > quant_eff(t256) * 1.12)
+        launch_ms<192, 256, 64, 2, 2, 2, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
+    else
+        launch_ms<256, 256, 64, 2, 2, 2, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
     hd_check_launch("linear_qkv_rope");
     return 0;
+}
+
+extern "C" int hd_linear_qkv_rope(const void *x, const void *wq, const void *wk, const void *wv,
+                                  const void *qn_w, const void *kn_w, const float *cs, void *q,
+                                  void *k, void *vt, int batch, int seq, int heads, int kv_heads,
+                                  int hidden, float eps) {
+    return hd_linear_qkv_rope_ws(x, wq, wk, wv, qn_w, kn_w, cs, q, k, vt, batch, seq, heads,
+                                 kv_heads, hidden, eps, nullptr, 0);
 }
 
 // Diagnostics: runs tuning-table configuration `cfg` (0..35) for
@@ -1517,11 +1569,13 @@ extern "C" void hd_linear_residual(const void *x, const void *w, const void *res
     hd_linear_residual_ws(x, w, res, y, M, N, K, nullptr, 0);
 }
 
-// Workspace for the tail split of one GEMM on the current device: half a
-// round of 256x256 fp32 partial tiles, split at most 8 ways.
+// Workspace for the tail split of one GEMM on the current device: one round
+// of 256x256 fp32 partial tiles (at most half a round of tiles, split up to
+// 8 ways, at most one round of chunks) plus bf16 staging of half a round of
+// tiles (the QKV epilogue pass).
 extern "C" int64_t hd_gemm_ws_bytes(void) {
-    const int slots = gemm_slots();
-    return (int64_t)(slots > 0 ? slots : 256) * 256 * 256 * 4;
+    const int64_t slots = gemm_slots() > 0 ? gemm_slots() : 256;
+    return slots * 256 * 256 * 4 + (slots / 2) * 256 * 256 * 2;
 }
 
 extern "C" void hd_linear_swiglu(const void *x, const void *wg, const void *wu, void *y, int M,

@@ -228,6 +228,7 @@ SIGNATURES = {
     "hd_gemm_tune_run": (c_int, [c_int, c_int, P, P, P, P, c_int, c_int, c_int]),
     "hd_gemm_set_family": (c_int, [c_int]),
     "hd_linear_qkv_rope": (c_int, [P, P, P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float]),
+    "hd_linear_qkv_rope_ws": (c_int, [P] * 10 + [c_int] * 5 + [c_float, P, ctypes.c_int64]),
     # hd_sdpa.h
     "hd_sdpa_create": (c_int, [ctypes.POINTER(c_void_p), c_int, c_int, c_int, c_int, c_int, c_int, c_float]),
     "hd_sdpa_execute": (c_int, [P, P, P, P, P, P, P]),

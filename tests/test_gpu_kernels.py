@@ -421,3 +421,43 @@ def test_gemm_tail_split(pkg, lib, dev, K, bias):
     assert same < 1.0                            # the tail did run split
     rel = float((c - want).norm() / want.norm())
     assert rel < 5e-3, rel
+
+
+def test_qkv_rope_tail_split(pkg, lib, dev):
+    """hd_linear_qkv_rope_ws at config 1's shape (B = 2, S = 4352: 34 x 24 =
+    816 tiles, three rounds of 256 CUs plus 48 tail tiles run as K chunks,
+    the merge running the same epilogue): whole tiles equal the unsplit
+    fused GEMM bit for bit, tail tiles to the fp32 reassociation of the K
+    sum carried through the norm and rotary."""
+    B, S, H, KV, HID, D = 2, 4352, 32, 8, 4096, 128
+    g = torch.Generator(device=dev).manual_seed(77)
+    x = (torch.randn(B * S, HID, generator=g, device=dev)).to(torch.bfloat16)
+    wq = (torch.randn(H * D, HID, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    wk = (torch.randn(KV * D, HID, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    wv = (torch.randn(KV * D, HID, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    qn = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    kn = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    posd = torch.from_numpy(grid_pos(256, 64, 64)).to(dev)
+    cs = pkg.rope_table(posd, S, D, theta=1e4)
+    ws = torch.empty(lib.hd_gemm_ws_bytes(), dtype=torch.uint8, device=dev)
+    outs = []
+    for use_ws in (False, True):
+        q = torch.zeros(B, H, S, D, dtype=torch.bfloat16, device=dev)
+        k = torch.zeros(B, KV, S, D, dtype=torch.bfloat16, device=dev)
+        vt = torch.zeros(B, KV, D, S, dtype=torch.bfloat16, device=dev)
+        args = [pkg.ptr(x), pkg.ptr(wq), pkg.ptr(wk), pkg.ptr(wv), pkg.ptr(qn), pkg.ptr(kn), pkg.ptr(cs),
+                pkg.ptr(q), pkg.ptr(k), pkg.ptr(vt), B, S, H, KV, HID, 1e-6]
+        rc = lib.hd_linear_qkv_rope_ws(*args, pkg.ptr(ws), ws.numel()) if use_ws else lib.hd_linear_qkv_rope(*args)
+        assert rc == 0
+        pkg.check_prim("qkv ws=%s" % use_ws)
+        torch.cuda.synchronize()
+        outs.append((q, k, vt))
+    fracs = []
+    for a, b in zip(*outs):
+        a, b = a.float(), b.float()
+        d = (a - b).abs()
+        fracs.append(float((d == 0).float().mean()))
+        assert float(d.norm() / a.norm()) < 2e-3
+        assert bool((d <= a.abs() * 2.0 ** -5 + 1e-2).all())
+    print("identical fractions q/k/vt:", fracs)
+    assert min(fracs) >= 0.9 and min(fracs) < 1.0
