@@ -54,6 +54,9 @@ def main():
     ap.add_argument("--layers", type=int, default=L)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=20)
+    ap.add_argument("--flash-only", action="store_true",
+                    help="run only the flash attention kernel at the configuration's shape "
+                         "(--kernel-iters launches), for rocprofv3 counter passes")
     ap.add_argument("--vision-only", action="store_true",
                     help="run only the vision tower of configuration 3 (3 references of 24x24 "
                          "patches, one multi-image call, 10 untimed + 10 timed), for rocprofv3")
@@ -83,6 +86,16 @@ def main():
     pkg.bind_torch_stream()
     if args.kernel_only:
         kernel_only(pkg, lib, B * S, args.kernel_iters)
+        return
+    if args.flash_only:
+        q = torch.randn(B, NH, S, D, device=dev).to(torch.bfloat16)
+        kk = torch.randn(B, NKV, S, D, device=dev).to(torch.bfloat16)
+        vt = torch.zeros(lib.hd_flash_vt_bytes(B, NKV, S) // 2, dtype=torch.bfloat16, device=dev)
+        ao = torch.empty(B, S, NH * D, dtype=torch.bfloat16, device=dev)
+        for _ in range(args.kernel_iters):
+            lib.hd_flash_attention(pkg.ptr(q), pkg.ptr(kk), pkg.ptr(vt), None, pkg.ptr(ao), B, NH, NKV,
+                                   S, D, 0, D ** -0.5, 1)
+        torch.cuda.synchronize()
         return
     if args.vision_only:
         from importlib import import_module as _im

@@ -134,6 +134,10 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
     const uint16_t *vbase = a.vt + ((size_t)b * a.Hkv + hk) * (size_t)FA_D * a.S_pad;
     // K tile: 64 rows x 16 chunks; wave instr i covers rows 4*(wave*4+i) ..+4
     // V^T tile: 128 rows x 8 chunks; wave instr i covers rows 8*(wave*4+i) ..+8
+    // LDS slots are XOR-swizzled so the 16 rows one ds_read_b128 phase
+    // touches land in 16 distinct 16-byte bank groups: chunk ^ (row & 15)
+    // for the 256-byte K rows, chunk ^ ((row >> 1) & 7) for the 128-byte V^T
+    // rows (two rows per 64-bank line)
     uint16_t *Ks0 = smem, *Vs0 = smem + 2 * FA_BK * FA_D;
     // buffer loads straight to LDS: per-lane byte offsets fixed for the
     // block, the tile advance goes in the scalar offset; K rows past S read
@@ -146,7 +150,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
         const int krow = (wave * 4 + i) * 4 + (lane >> 4);
         k_vo[i] = (uint32_t)(krow * FA_D + (((lane & 15) ^ (krow & 15)) * 8)) * 2;
         const int vrow = (wave * 4 + i) * 8 + (lane >> 3);
-        v_vo[i] = (uint32_t)(vrow * a.S_pad + (((lane & 7) ^ (vrow & 7)) * 8)) * 2;
+        v_vo[i] = (uint32_t)(vrow * a.S_pad + (((lane & 7) ^ ((vrow >> 1) & 7)) * 8)) * 2;
     }
     auto issue = [&](int t, int buf) {
         uint16_t *Ks = Ks0 + buf * FA_BK * FA_D, *Vs = Vs0 + buf * FA_D * FA_BK;
@@ -249,7 +253,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
 #pragma unroll
             for (int dt = 0; dt < 4; dt++) {
                 const int row = dt * 32 + l32;
-                const int c = ((st * 2 + h) ^ (row & 7)) * 8;
+                const int c = ((st * 2 + h) ^ ((row >> 1) & 7)) * 8;
                 bf16x8_t vf = *(const bf16x8_t *)(Vs + row * FA_BK + c);
                 o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[st], o[dt], 0, 0, 0);
             }
