@@ -81,6 +81,10 @@ void hd_linear_residual(const void *x_dev, const void *w_dev,
  * with the SwiGLU epilogue; the gate and up products never reach HBM. */
 void hd_linear_swiglu(const void *x_dev, const void *wg_dev,
                       const void *wu_dev, void *y_dev, int M, int F, int K);
+/* Extension: hd_linear_swiglu with the tail-split workspace of
+ * hd_linear_residual_ws. */
+void hd_linear_swiglu_ws(const void *x_dev, const void *wg_dev, const void *wu_dev, void *y_dev,
+                         int M, int F, int K, void *ws, int64_t ws_bytes);
 
 /* y[M, N0+N1+N2] = x . [W0;W1;W2]^T with three separately stored weight
  * matrices (the q/k/v projections) computed as one GEMM; every Ni must be

@@ -173,7 +173,7 @@ static hd_status block_core(const void *in, const float *cs, const void *mask, i
         hd_status st = copy_d2d(ints->post_ln, s.ln, (size_t)M * HID * 2);
         if (st != HD_OK) return st;
     }
-    hd_linear_swiglu(s.ln, bw->gate_proj, bw->up_proj, s.swi, M, FF, HID);
+    hd_linear_swiglu_ws(s.ln, bw->gate_proj, bw->up_proj, s.swi, M, FF, HID, s.fa_ws, s.fa_ws_bytes);
     if (ints && ints->mlp_out) hd_linear(s.swi, bw->down_proj, nullptr, ints->mlp_out, M, HID, FF, 1);
     hd_linear_residual_ws(s.swi, bw->down_proj, s.ar, out, M, HID, FF, s.fa_ws, s.fa_ws_bytes);
     return launch_status("launch");

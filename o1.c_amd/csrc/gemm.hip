@@ -1578,10 +1578,10 @@ extern "C" int64_t hd_gemm_ws_bytes(void) {
     return slots * 256 * 256 * 4 + (slots / 2) * 256 * 256 * 2;
 }
 
-extern "C" void hd_linear_swiglu(const void *x, const void *wg, const void *wu, void *y, int M,
-                                 int F, int K) {
+extern "C" void hd_linear_swiglu_ws(const void *x, const void *wg, const void *wu, void *y, int M,
+                                    int F, int K, void *ws, int64_t ws_bytes) {
     if (!x || !wg || !wu || !y || M <= 0 || F <= 0 || K <= 0 || !mfma_ok(x, y, F, K) ||
-        F % 64) {
+        F % 64 || (ws && (uintptr_t)ws % 16)) {
         snprintf(hd_cuda_errbuf(), 512, "linear_swiglu: bad args");
         return;
     }
@@ -1593,8 +1593,13 @@ extern "C" void hd_linear_swiglu(const void *x, const void *wg, const void *wu, 
     g.seg_end[0] = g.seg_end[1] = g.seg_end[2] = F;
     g.C = (uint16_t *)y;
     g.M = M; g.N = F; g.K = K; g.ldc = F;
-    gemm_launch(EPI_SWIGLU, g);
+    gemm_launch(EPI_SWIGLU, g, ws, ws ? ws_bytes : 0);
     hd_check_launch("linear_swiglu");
+}
+
+extern "C" void hd_linear_swiglu(const void *x, const void *wg, const void *wu, void *y, int M,
+                                 int F, int K) {
+    hd_linear_swiglu_ws(x, wg, wu, y, M, F, K, nullptr, 0);
 }
 
 extern "C" void hd_linear_concat3(const void *x, const void *w0, int N0, const void *w1, int N1,

@@ -223,6 +223,7 @@ SIGNATURES = {
     "hd_gemm_set_prod_backend": (None, [c_int]),
     "hd_linear_residual": (None, [P, P, P, P, c_int, c_int, c_int]),
     "hd_linear_swiglu": (None, [P, P, P, P, c_int, c_int, c_int]),
+    "hd_linear_swiglu_ws": (None, [P, P, P, P, c_int, c_int, c_int, P, ctypes.c_int64]),
     "hd_linear_concat3": (None, [P, P, c_int, P, c_int, P, c_int, P, c_int, c_int]),
     "hd_gemm_config_name": (c_char_p, [c_int, c_int, c_int, c_int]),
     "hd_gemm_tune_run": (c_int, [c_int, c_int, P, P, P, P, c_int, c_int, c_int]),

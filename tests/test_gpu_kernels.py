@@ -461,3 +461,28 @@ def test_qkv_rope_tail_split(pkg, lib, dev):
         assert bool((d <= a.abs() * 2.0 ** -5 + 1e-2).all())
     print("identical fractions q/k/vt:", fracs)
     assert min(fracs) >= 0.9 and min(fracs) < 1.0
+
+
+def test_swiglu_tail_split(pkg, lib, dev):
+    """hd_linear_swiglu_ws at config 2's row count (M = 16640: 65 x 96 =
+    6240 tiles, 24 rounds + 96 tail tiles in K chunks): whole tiles equal
+    the unsplit GEMM bit for bit, the tail within the reassociation of the
+    K sum carried through silu(gate) * up."""
+    M, F, K = 16640, 12288, 4096
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(F, K, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    wu = (torch.randn(F, K, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    ws = torch.empty(lib.hd_gemm_ws_bytes(), dtype=torch.uint8, device=dev)
+    y0 = torch.empty(M, F, dtype=torch.bfloat16, device=dev)
+    y1 = torch.empty_like(y0)
+    lib.hd_linear_swiglu(pkg.ptr(x), pkg.ptr(wg), pkg.ptr(wu), pkg.ptr(y0), M, F, K)
+    lib.hd_linear_swiglu_ws(pkg.ptr(x), pkg.ptr(wg), pkg.ptr(wu), pkg.ptr(y1), M, F, K, pkg.ptr(ws), ws.numel())
+    pkg.check_prim("swiglu tail split")
+    torch.cuda.synchronize()
+    a, b = y0.float(), y1.float()
+    d = (a - b).abs()
+    same = float((d == 0).float().mean())
+    print("identical fraction", same)
+    assert same >= 6144 / 6240 - 1e-3 and same < 1.0
+    assert float(d.norm() / a.norm()) < 1e-3
