@@ -1196,12 +1196,14 @@ static int gemm_slots() {
     return cus;
 }
 
-// Tail split plan for `units` tiles of nk K tiles: the tiles of the last,
-// partly filled round run as P K chunks (2..8) when that round is at most
-// half full and the partial tiles fit in ws_bytes. Returns P (1: no split).
+// Tail split plan for `units` tiles of nk K tiles on `occ` blocks per CU:
+// the tiles of the last, partly filled round (all tiles when there are
+// fewer than half a round) run as P K chunks (2..8) when that round is at
+// most half full and the partial tiles fit in ws_bytes. Returns P (1: no
+// split).
 static int tail_split_of(long units, int nk, size_t tile_bytes, int64_t ws_bytes,
-                         size_t stage_bytes = 0) {
-    const int slots = gemm_slots();
+                         size_t stage_bytes = 0, int occ = 1) {
+    const int slots = gemm_slots() * occ;
     if (slots <= 0 || ws_bytes <= 0) return 1;
     const long rem = units % slots;
     if (rem == 0 || rem > slots / 2) return 1;
@@ -1220,10 +1222,10 @@ static void launch_ms(GemmArgs &g, void *ws = nullptr, int64_t ws_bytes = 0) {
     g.ntn = (g.N + Cfg::BN_OUT - 1) / Cfg::BN_OUT;
     const long units = (long)g.ntm * g.ntn;
     int P = 1;
-    if (ws && MF == 32 && OCC == 1)
+    if (ws && MF == 32)
         P = tail_split_of(units, g.K / BK, (size_t)BM * BN * 4, ws_bytes,
-                          EPI == EPI_QKV ? (size_t)BM * BN * 2 : 0);
-    const long n_tail = P > 1 ? units % gemm_slots() : 0;
+                          EPI == EPI_QKV ? (size_t)BM * BN * 2 : 0, OCC);
+    const long n_tail = P > 1 ? units % ((long)gemm_slots() * OCC) : 0;
     g.n_whole = (int)(units - n_tail);
     g.split = P;
     g.part = (float *)ws;
@@ -1323,7 +1325,7 @@ static const char *pick_and_launch(GemmArgs &g, bool launch, void *ws = nullptr,
     const long t256 = (long)((g.M + 255) / 256) * tn;
     const long t192 = (long)((g.M + 191) / 192) * tn;
     if (t256 < 512) {
-        if (launch) launch_ms<128, 128, 64, 2, 2, 2, EPI, 1, 2>(g);
+        if (launch) launch_ms<128, 128, 64, 2, 2, 2, EPI, 1, 2>(g, ws, ws_bytes);
         return "bf16_128x128x64_w2x2_occ2";
     }
     // K <= 8192: 4 waves of 128x128 with one fragment ring across the K loop;

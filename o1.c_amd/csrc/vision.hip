@@ -351,7 +351,7 @@ void gelu_padded(void *x, int rows, int cols, int ld) {
 
 // ---- workspace layout ----
 struct Layout {
-    int64_t h, ar, ln, tmp, qkv, q, k, v, vt, f1, w2, cs, sn, total;
+    int64_t h, ar, ln, tmp, qkv, q, k, v, vt, f1, w2, cs, sn, gws, total;
 };
 
 int64_t al(int64_t b) { return (b + 255) & ~(int64_t)255; }
@@ -377,6 +377,7 @@ Layout layout_of(int64_t R, int64_t n) {
     L.w2 = b; b += al((int64_t)kH * kIP * 2);
     L.cs = b; b += al(n * kD * 4);
     L.sn = b; b += al(n * kD * 4);
+    L.gws = b; b += al(hd_gemm_ws_bytes());   // split-K partials of the small GEMMs
     L.total = b;
     return L;
 }
@@ -719,12 +720,14 @@ static hd_status forward_impl(const hd_vision_binding *bw, hd_vision_workspace *
     uint16_t *vt = (uint16_t *)(base + L.vt), *f1 = (uint16_t *)(base + L.f1);
     uint16_t *w2 = (uint16_t *)(base + L.w2);
     float *cs = (float *)(base + L.cs), *sn = (float *)(base + L.sn);
+    void *gws = base + L.gws;
+    const int64_t gwsb = hd_gemm_ws_bytes();
     hipStream_t st = hd_stream();
     const size_t nH = (size_t)N * kH * 2;
     hd_status s;
 
     // patch embed + position embedding, rotary tables
-    hd_linear(pixel_values, bw->patch_proj_w, bw->patch_proj_b, tmp, N, kH, HD_VISION_PATCH_DIM, 1);
+    hd_linear_ws(pixel_values, bw->patch_proj_w, bw->patch_proj_b, tmp, N, kH, HD_VISION_PATCH_DIM, gws, gwsb);
     v_embed_kernel<<<hd_cdiv((size_t)N * (kH / 8), 256), 256, 0, st>>>(
         tmp, (const uint16_t *)bw->pos_embed, (const int *)ws->pos_idx, (const float *)ws->pos_wgt,
         nullptr, h, N, n, kH);
@@ -741,7 +744,7 @@ static hd_status forward_impl(const hd_vision_binding *bw, hd_vision_workspace *
             snap(s0[HD_B0_INPUT], h, nH);
             snap(s0[HD_B0_NORM1], ln, nH);
         }
-        hd_linear(ln, b->qkv_w, b->qkv_b, qkv, N, kQKV, kH, 1);
+        hd_linear_ws(ln, b->qkv_w, b->qkv_b, qkv, N, kQKV, kH, gws, gwsb);
         if (s0) snap(s0[HD_B0_QKV], qkv, (size_t)N * kQKV * 2);
         v_qkv_rope_pad_kernel<<<hd_cdiv((size_t)R * kNH * n * kDP, 256), 256, 0, st>>>(
             qkv, cs, sn, q, k, v, R, n, kNH, kD, kDP);
@@ -759,7 +762,7 @@ static hd_status forward_impl(const hd_vision_binding *bw, hd_vision_workspace *
         }
         v_unpad_heads_kernel<<<hd_cdiv((size_t)N * kH, 256), 256, 0, st>>>(qkv, ln, N, kNH, kD, kDP);
         if (s0) snap(s0[HD_B0_ATTN_MERGED], ln, nH);
-        hd_linear(ln, b->proj_w, b->proj_b, tmp, N, kH, kH, 1);
+        hd_linear_ws(ln, b->proj_w, b->proj_b, tmp, N, kH, kH, gws, gwsb);
         if (s0) snap(s0[HD_B0_PROJ], tmp, nH);
         // attn_resid = bf16(h + proj); ln = LayerNorm2(attn_resid)
         layernorm(h, tmp, ar, b->norm2_w, b->norm2_b, ln, N, kH, eps);
@@ -772,7 +775,7 @@ static hd_status forward_impl(const hd_vision_binding *bw, hd_vision_workspace *
         if (s0) snap(s0[HD_B0_FC1], f1, (size_t)N * kIP * 2);
         v_pad_rows_kernel<<<hd_cdiv((size_t)kH * (kIP / 8), 256), 256, 0, st>>>(
             (const uint16_t *)b->fc2_w, w2, kH, kI, kIP);
-        hd_linear(f1, w2, b->fc2_b, tmp, N, kH, kIP, 1);
+        hd_linear_ws(f1, w2, b->fc2_b, tmp, N, kH, kIP, gws, gwsb);
         if (s0) snap(s0[HD_B0_FC2], tmp, nH);
         // h = bf16(attn_resid + fc2), then the next LayerNorm (next block's
         // norm1, or the final merger's norm over 1152)
@@ -793,12 +796,12 @@ static hd_status forward_impl(const hd_vision_binding *bw, hd_vision_workspace *
             uint16_t *dn = ar;                 // [m, 4608] == [N, 1152]; attn_resid is dead here
             layernorm(h, nullptr, nullptr, d->norm_w, d->norm_b, dn, m, kU * kH, eps);
             snap(sd[0], dn, nH);
-            hd_linear(dn, d->fc1_w, d->fc1_b, f1, m, kU * kH, kU * kH, 1);
+            hd_linear_ws(dn, d->fc1_w, d->fc1_b, f1, m, kU * kH, kU * kH, gws, gwsb);
             snap(sd[1], f1, (size_t)m * kU * kH * 2);
             gelu_padded<false>(f1, m, kU * kH, kU * kH);
             snap(sd[2], f1, (size_t)m * kU * kH * 2);
             if (deepstack_out[ds_j])
-                hd_linear(f1, d->fc2_w, d->fc2_b, deepstack_out[ds_j], m, kO, kU * kH, 1);
+                hd_linear_ws(f1, d->fc2_w, d->fc2_b, deepstack_out[ds_j], m, kO, kU * kH, gws, gwsb);
             if (deepstack_out[ds_j]) snap(sd[3], deepstack_out[ds_j], (size_t)m * kO * 2);
             if ((s = launch_err("deepstack merger")) != HD_OK) return s;
         }
@@ -808,11 +811,11 @@ static hd_status forward_impl(const hd_vision_binding *bw, hd_vision_workspace *
     void **sm = ws->merger_snaps;
     snap(sm[0], ln, nH);
     snap(sm[1], ln, nH);
-    hd_linear(ln, bw->merger.fc1_w, bw->merger.fc1_b, f1, m, kU * kH, kU * kH, 1);
+    hd_linear_ws(ln, bw->merger.fc1_w, bw->merger.fc1_b, f1, m, kU * kH, kU * kH, gws, gwsb);
     snap(sm[2], f1, (size_t)m * kU * kH * 2);
     gelu_padded<false>(f1, m, kU * kH, kU * kH);
     snap(sm[3], f1, (size_t)m * kU * kH * 2);
-    hd_linear(f1, bw->merger.fc2_w, bw->merger.fc2_b, image_embeds_out, m, kO, kU * kH, 1);
+    hd_linear_ws(f1, bw->merger.fc2_w, bw->merger.fc2_b, image_embeds_out, m, kO, kU * kH, gws, gwsb);
     snap(sm[4], image_embeds_out, (size_t)m * kO * 2);
     return launch_err("merger");
 }

@@ -243,8 +243,10 @@ def test_vision_tower_vs_oracle(pkg, lib, dev, vision_weights, grid):
 
 
 def test_vision_multi_matches_single(pkg, lib, dev, vision_weights):
-    """hd_vision_forward_multi over 3 images equals 3 hd_vision_forward calls
-    row for row (per-row GEMM, per-image attention: same arithmetic)."""
+    """hd_vision_forward_multi over 3 images against 3 hd_vision_forward
+    calls: the same arithmetic up to the K chunking of the small GEMMs
+    (split-K by tile count, which differs with the row count), so within the
+    tower's rounding spread; and a repeated call is bit-identical."""
     gh, gw, R = 6, 10, 3
     n, m = gh * gw, gh * gw // 4
     vb = vision_binding(pkg, vision_weights)
@@ -272,9 +274,15 @@ def test_vision_multi_matches_single(pkg, lib, dev, vision_weights):
                                                px[r * n:].data_ptr(), n, gh, gw, pkg.ptr(e1), p1),
                          "single")
         torch.cuda.synchronize()
-        assert torch.equal(e1, emb[r * m:(r + 1) * m]), r
-        for j in range(3):
-            assert torch.equal(d1[j], ds[j][r * m:(r + 1) * m]), (r, j)
+        pairs = [(e1, emb[r * m:(r + 1) * m])] + [(d1[j], ds[j][r * m:(r + 1) * m]) for j in range(3)]
+        for a_, b_ in pairs:
+            a_, b_ = host(a_), host(b_)
+            assert rel_l2(a_, b_) < 3e-2 and cosine(a_, b_) > 0.9998, r
+    emb2 = torch.empty_like(emb)
+    pkg.check_status(lib.hd_vision_forward_multi(ctypes.byref(vb), ctypes.byref(wss[1]), pkg.ptr(px), R,
+                                                 n, gh, gw, pkg.ptr(emb2), None), "multi again")
+    torch.cuda.synchronize()
+    assert torch.equal(emb, emb2)
 
 
 def test_forward_with_visual_vs_oracle(pkg, lib, dev):
