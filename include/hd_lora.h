@@ -18,6 +18,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "hd_weights.h"
 #include "hidream_hip.h"
 
 #ifdef __cplusplus
@@ -39,6 +40,39 @@ typedef struct {
     void *up_dev;
     void *base_dev;
 } hd_lora_entry;
+
+/* include/hd_lora.h:47-61 */
+typedef struct {
+    hd_lora_entry *entries;
+    size_t count;
+    char sha256[65];
+    char base_profile[16];
+} hd_lora_adapter;
+
+typedef struct {              /* one adapter path and its multiplier */
+    const char *path;
+    float multiplier;
+} hd_lora_spec;
+
+typedef struct {
+    const hd_lora_spec *items;
+    size_t count;
+} hd_lora_config;
+
+/* include/hd_lora.h:71 (src/model/lora.c:126-375): parses every adapter
+ * (musubi .safetensors: "<prefix>.lora_down.weight" [rank, in],
+ * "<prefix>.lora_up.weight" [out, rank], optional scalar "<prefix>.alpha",
+ * default alpha = rank; BF16 / F16 / F32), validates every target against
+ * the dev profile's 257 linear layers and the store, then uploads the
+ * factors as fp32 and merges them into the store's bf16 weights in place on
+ * store->upload_stream (synchronised before returning). A parse or
+ * validation error returns before any weight is touched. Each entry takes
+ * the factors of its own adapter (the reference fills a target named by two
+ * adapters from the first one it reads for both). count == 0 is a no-op. */
+hd_status hd_lora_apply(const hd_lora_config *cfg, hd_weight_store *store, int device_id);
+
+/* include/hd_lora.h:79: last error of hd_lora_apply. */
+const char *hd_lora_last_error(void);
 
 /* include/hd_lora.h:75. `stream` is a hipStream_t (NULL = library stream).
  * Returns HD_OK, HD_ERR_MISSING on a null pointer, HD_ERR_UNSUPPORTED on a

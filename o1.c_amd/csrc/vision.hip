@@ -383,7 +383,7 @@ Layout layout_of(int64_t R, int64_t n) {
 }
 
 void snap(void *dst, const void *src, size_t bytes) {
-    if (dst) hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, hd_stream());
+    if (dst) (void)hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, hd_stream());
 }
 
 hd_status launch_err(const char *what) {

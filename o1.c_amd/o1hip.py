@@ -16,6 +16,7 @@ c_void_p, c_int, c_int64, c_float, c_size_t, c_char_p = (
     ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t, ctypes.c_char_p)
 
 HD_OK, HD_ERR_MISSING, HD_ERR_OOM, HD_ERR_RUNTIME, HD_ERR_UNSUPPORTED = 0, 6, 7, 8, 9
+HD_ERR_IO, HD_ERR_PARSE = 1, 2
 HD_ERR_MISMATCH = 5
 
 
@@ -168,6 +169,14 @@ class hd_visual_cond(ctypes.Structure):
                 ("v_tokens", c_int)]
 
 
+class hd_lora_spec(ctypes.Structure):
+    _fields_ = [("path", ctypes.c_char_p), ("multiplier", c_float)]
+
+
+class hd_lora_config(ctypes.Structure):
+    _fields_ = [("items", ctypes.POINTER(hd_lora_spec)), ("count", c_size_t)]
+
+
 P = c_void_p
 # name -> (restype, argtypes); every symbol include/*.h declares.
 SIGNATURES = {
@@ -282,6 +291,8 @@ SIGNATURES = {
                                    c_int, c_int, c_int, c_int, ctypes.POINTER(hd_forward_diagnostics), P, P]),
     # hd_lora.h
     "hd_lora_merge_gpu": (c_int, [ctypes.POINTER(hd_lora_entry), c_size_t, P]),
+    "hd_lora_apply": (c_int, [ctypes.POINTER(hd_lora_config), ctypes.POINTER(hd_weight_store), c_int]),
+    "hd_lora_last_error": (c_char_p, []),
     # hd_host.h
     "hd_torch_rng_seed": (None, [ctypes.POINTER(hd_torch_rng), ctypes.c_uint64]),
     "hd_torch_rng_u32": (ctypes.c_uint32, [ctypes.POINTER(hd_torch_rng)]),
