@@ -24,6 +24,9 @@ PEAK_BF16 = 2.5e15      # dense bf16 MFMA, MI355X
 PEAK_HBM = 8.0e12
 
 CFGS = {
+    # one decoder block (the reference's CPU-runnable case): 32x32 image
+    # tokens + 128 text tokens, batch 1
+    "c0": dict(name="block_forward_s1152", batch=1, text=128, gh=32, gw=32, refs=0),
     "c1": dict(name="denoise_step_1024sq_cfg2", batch=2, text=256, gh=64, gw=64, refs=0),
     "c2": dict(name="denoise_step_2048sq", batch=1, text=256, gh=128, gw=128, refs=0),
     # multi-reference edit: 64x64 target + 3 references of 64x64 (+64 RoPE
@@ -86,6 +89,9 @@ def main():
     pkg.bind_torch_stream()
     if args.kernel_only:
         kernel_only(pkg, lib, B * S, args.kernel_iters)
+        return
+    if args.config == "c0":
+        run_c0(pkg, lib, cfg, args, dev)
         return
     if args.flash_only:
         q = torch.randn(B, NH, S, D, device=dev).to(torch.bfloat16)
@@ -226,7 +232,8 @@ def main():
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(S, T, gh, gw, B, args.layers)
 
-    metric = {"c1": "DiT denoise steps/sec (1024^2, CFG batch 2, 36 blocks)",
+    metric = {"c0": "DiT block forwards/sec (config 0)",
+              "c1": "DiT denoise steps/sec (1024^2, CFG batch 2, 36 blocks)",
               "c2": "DiT denoise steps/sec (2048^2, 36 blocks)",
               "c3": "DiT edit steps/sec (1024^2 target + 3 references, 36 blocks)",
               "c4": "DiT denoise steps/sec (1024^2, CFG batch 2) + LoRA merge and 28-step image"}
@@ -260,6 +267,91 @@ def main():
         "cpu_baseline": cpu,
     }
     res.update(extra)
+    print(json.dumps(res))
+
+
+def run_c0(pkg, lib, cfg, args, dev):
+    """Configuration 0: one decoder block through hd_decoder_block_batched
+    (B = 1, S = 1152: 32x32 image tokens + 128 text tokens at position 0,
+    2-D RoPE theta 1e4), random-init bf16 weights (seed 0), N(0,1) input
+    (seed 1). A step is one block forward."""
+    import numpy as np
+    import torch
+    from importlib import import_module
+    synth = import_module("o1c_amd.synthetic")
+    T, gh, gw = cfg["text"], cfg["gh"], cfg["gw"]
+    S = T + gh * gw
+    tensors = synth.build_model(n_layers=1, seed=0, device="cuda:0")
+    model = synth.Model(tensors, 1)
+    pkg.set_block_config(theta=1e4)
+    pos = np.zeros((3, S), np.float32)
+    one = (ctypes.c_int * 1)
+    assert lib.hd_seq_grid_positions(T, 1, one(gh), one(gw), one(0), None, 0.0, pkg.np_ptr(pos)) == S
+    cs = pkg.rope_table(torch.from_numpy(pos).to(dev), S, D, theta=1e4)
+    x = torch.randn(S, HID, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(dev)
+    out = torch.empty_like(x)
+    sb = lib.hd_decoder_block_batched_scratch_bytes(1, S, NH, NKV, HID, FF, D)
+    scr = torch.empty(sb, dtype=torch.uint8, device=dev)
+    blk = ctypes.byref(model.binding.blocks[0])
+
+    def step():
+        st = lib.hd_decoder_block_batched(pkg.ptr(x), pkg.ptr(cs), None, 0, blk, pkg.ptr(scr), sb, None,
+                                          pkg.ptr(out), 1, S, NH, NKV, HID, FF, D)
+        if st != 0:
+            raise RuntimeError(lib.hd_last_error().decode())
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+    gemm_tok = 2 * (HID * NH * D + 2 * HID * NKV * D + NH * D * HID + 3 * HID * FF)
+    flops = S * gemm_tok + 4 * S * S * NH * D
+    # dominant kernel at this shape: the gate/up GEMM + SwiGLU (M = 1152)
+    xl = torch.randn(S, HID, device=dev).to(torch.bfloat16)
+    sw = torch.empty(S, FF, dtype=torch.bfloat16, device=dev)
+    b0 = model.binding.blocks[0]
+    for _ in range(3):
+        lib.hd_linear_swiglu(pkg.ptr(xl), ctypes.c_void_p(b0.gate_proj), ctypes.c_void_p(b0.up_proj), pkg.ptr(sw), S, FF, HID)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(args.kernel_iters):
+        lib.hd_linear_swiglu(pkg.ptr(xl), ctypes.c_void_p(b0.gate_proj), ctypes.c_void_p(b0.up_proj), pkg.ptr(sw), S, FF, HID)
+    e1.record()
+    torch.cuda.synchronize()
+    kms = e0.elapsed_time(e1) / args.kernel_iters
+    kflop = 2.0 * S * 2 * FF * HID
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(S, T, gh, gw, 1, 1)
+        cpu["unit"] = "blocks/s"
+        cpu["sample"] = cpu["sample"].replace("steps/s = 1/(t_block x 1 blocks x 1 CFG sequences)",
+                                              "blocks/s = 1/t_block")
+    res = {
+        "metric": "DiT block forwards/sec (config 0: one decoder block, S=1152)",
+        "value": round(1000.0 / ms, 3), "unit": "blocks/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init bf16 weights seed 0, N(0,1) input seed 1)",
+        "config": {"workload": cfg["name"], "batch": 1, "seq_len": S, "image_tokens": gh * gw,
+                   "text_tokens": T, "layers": 1, "hidden": HID, "heads": NH, "kv_heads": NKV,
+                   "ffn": FF, "parallelism": "single GPU"},
+        "step_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+        "step_mfma_frac": round(flops / (ms * 1e-3) / PEAK_BF16, 4),
+        "wall_s": round(wall, 3),
+        "roofline": {"kernel": "gemm_bf16 gate/up + SwiGLU epilogue", "bound": "mfma",
+                     "achieved": round(kflop / (kms * 1e-3) / 1e12, 1), "peak": PEAK_BF16 / 1e12,
+                     "unit": "TFLOP/s", "frac": round(kflop / (kms * 1e-3) / PEAK_BF16, 4),
+                     "traffic": None, "launch_ms": round(kms, 4), "shape": [S, 2 * FF, HID]},
+        "cpu_baseline": cpu,
+    }
     print(json.dumps(res))
 
 

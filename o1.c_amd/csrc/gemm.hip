@@ -1318,15 +1318,45 @@ static double quant_eff(long tiles) {
     return (double)tiles / (double)(rounds * 256);
 }
 
+// Estimated time (s) of a tile family: rounds of resident blocks, each the
+// time of `occ` tiles on a CU (2*BM*BNA*K flops at ~half the per-CU peak x
+// the family's relative per-flop efficiency: 192-row tiles 8-18 % slower
+// per flop than 256-row ones, 128x128 tiles at two per CU ~20 %); with the
+// tail split the last round is one chunk plus the merge (the fp32 partials
+// written and read once at HBM rate, and a launch).
+static double tile_cost(long units, int occ, int BM, int BNA, int K, double eff, int P) {
+    const long slots = (long)(gemm_slots() > 0 ? gemm_slots() : 256) * occ;
+    const double rate = 2.5e15 / 256 * 0.5 * eff;
+    const double t_round = occ * 2.0 * BM * BNA * (double)K / rate;
+    const long full = units / slots, rem = units % slots;
+    double t = full * t_round;
+    if (rem) {
+        if (P > 1)
+            t += t_round / P + (double)rem * P * BM * BNA * 8.0 / 8e12 + 4e-6;
+        else
+            t += t_round;
+    }
+    return t;
+}
+
 template <int EPI>
 static const char *pick_and_launch(GemmArgs &g, bool launch, void *ws = nullptr, int64_t ws_bytes = 0) {
     const int bn_out = EPI == EPI_SWIGLU ? 128 : 256;
     const long tn = (g.N + bn_out - 1) / bn_out;
     const long t256 = (long)((g.M + 255) / 256) * tn;
     const long t192 = (long)((g.M + 191) / 192) * tn;
-    if (t256 < 512) {
+    const long t128 = (long)((g.M + 127) / 128) * ((g.N + bn_out / 2 - 1) / (bn_out / 2));
+    const int nk = g.K / 64;
+    // tail split plans (P = 1: none) of the three tile families
+    const int p256 = ws ? tail_split_of(t256, nk, (size_t)256 * 256 * 4, ws_bytes) : 1;
+    const int p192 = ws ? tail_split_of(t192, nk, (size_t)192 * 256 * 4, ws_bytes) : 1;
+    const int p128 = ws ? tail_split_of(t128, nk, (size_t)128 * 128 * 4, ws_bytes, 0, 2) : 1;
+    const double c256 = tile_cost(t256, 1, 256, 256, g.K, 1.0, p256);
+    const double c192 = tile_cost(t192, 1, 192, 256, g.K, 0.9, p192);
+    const double c128 = tile_cost(t128, 2, 128, 128, g.K, 0.8, p128);
+    if (c128 < c256 && c128 < c192) {
         if (launch) launch_ms<128, 128, 64, 2, 2, 2, EPI, 1, 2>(g, ws, ws_bytes);
-        return "bf16_128x128x64_w2x2_occ2";
+        return p128 > 1 ? "bf16_128x128x64_w2x2_occ2_split" : "bf16_128x128x64_w2x2_occ2";
     }
     // K <= 8192: 4 waves of 128x128 with one fragment ring across the K loop;
     // deeper K: 8 interleaved waves. Operands through buffer loads straight
@@ -1334,13 +1364,7 @@ static const char *pick_and_launch(GemmArgs &g, bool launch, void *ws = nullptr,
     const bool fits = (size_t)(g.M + 256) * g.K * 2 < ((size_t)1 << 31) &&
                       (size_t)g.N * g.K * 2 < ((size_t)1 << 31);
     const bool ring = g_family == 0 && g.K <= 8192 && fits;
-    // With a workspace, a last round that is at most half full runs as K
-    // chunks of its tiles (tail split): 256-row tiles then keep their
-    // per-flop efficiency (192-row tiles are 8-18 % slower per flop) at the
-    // quantisation cost of a fraction of a round.
-    const bool split256 = ws && tail_split_of(t256, g.K / 64, (size_t)256 * 256 * 4, ws_bytes) > 1;
-    // otherwise 192-row tiles when they quantise the grid enough better
-    const bool use192 = !split256 && quant_eff(t192) > quant_eff(t256) * 1.12;
+    const bool use192 = c192 < c256;
     if (use192) {
         if (ring) {
             if (launch) launch_ms<192, 256, 64, 2, 2, 2, EPI, 3, 1, 5>(g, ws, ws_bytes);
@@ -1353,6 +1377,7 @@ static const char *pick_and_launch(GemmArgs &g, bool launch, void *ws = nullptr,
         if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 1>(g, ws, ws_bytes);
         return "bf16_192x256x64_w2x4_ilv";
     }
+    const bool split256 = p256 > 1;
     if (ring) {
         if (launch) launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 5>(g, ws, ws_bytes);
         return split256 ? "bf16_256x256x64_w2x2_ring_buf_tailsplit" : "bf16_256x256x64_w2x2_ring_buf";
