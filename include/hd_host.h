@@ -179,6 +179,27 @@ hd_status hd_denoise(const hd_forward_binding *bw, hd_forward_workspace *ws, int
                      int ff_hidden, int head_dim, int tms_token_id, void *scratch,
                      int64_t scratch_bytes, void *stream);
 
+/* hd_denoise_visual: the edit / personalize loop (generate.c:855-935), batch
+ * 1 with vision conditioning. Each step runs hd_forward over
+ * [text | target img_tokens | ref_tokens references] with `mask` (or the
+ * workspace's SDPA plan) and `visual`, takes the velocity of the target rows
+ * only and applies the sampler to z [img_tokens, 3072] in place. The
+ * references are `ref_patches` [ref_tokens, 3072] bf16, copied once behind
+ * the target rows, unless the workspace caches their x_embedder rows
+ * (ws->xe_ref with ws->n_ref == ref_tokens, as generate.c:792-805 sets up):
+ * then the cache is used and ref_patches may be NULL. The reference's edit loop runs the flash step for its default
+ * schedule: pass HD_SAMPLER_FLASH with a hd_scheduler_derive_default
+ * schedule for that. Scratch: hd_denoise_run_scratch_bytes(1, seq,
+ * img_tokens + ref_tokens, steps). */
+hd_status hd_denoise_visual(const hd_forward_binding *bw, hd_forward_workspace *ws, int sampler,
+                            const hd_scheduler *sched, int steps, const int64_t *ids_dev,
+                            int text_len, const float *pos_dev, const void *mask_dev,
+                            const hd_visual_cond *visual, void *z_dev, int img_tokens,
+                            const void *ref_patches, int ref_tokens, uint64_t seed,
+                            float s_noise_start, float s_noise_end, float noise_clip_std, int seq,
+                            int heads, int kv_heads, int hidden, int ff_hidden, int head_dim,
+                            int tms_token_id, void *scratch, int64_t scratch_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

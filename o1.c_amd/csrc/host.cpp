@@ -589,20 +589,18 @@ struct PinnedNoise {
 };
 }  // namespace
 
-extern "C" hd_status hd_denoise(const hd_forward_binding *bw, hd_forward_workspace *ws, int sampler,
-                                const hd_scheduler *sched, int steps, int B, const int64_t *ids,
-                                int T, const float *pos, int ar_len, void *z, int I,
-                                float guidance, uint64_t seed, float sn_start, float sn_end,
-                                float clip, int S, int H, int KV, int HID, int FF, int D, int tms,
-                                void *scratch, int64_t scratch_bytes, void *stream) {
-    if (!bw || !ws || !sched || !ids || !pos || !z || !scratch || I <= 0 || steps < 1) {
-        hd_set_error("denoise: null argument");
-        return HD_ERR_MISSING;
-    }
-    if ((B != 1 && B != 2) || sampler < HD_SAMPLER_EULER || sampler > HD_SAMPLER_UNIPC) {
-        hd_set_error("denoise: batch must be 1 or 2 and sampler 0..2");
-        return HD_ERR_UNSUPPORTED;
-    }
+// Shared loop of hd_denoise / hd_denoise_visual. I_t target rows are
+// denoised; with n_ref reference rows the forward sees I_t + n_ref image
+// tokens (target first), the references either as patches copied once after
+// the target rows (`ref`) or as cached x_embedder rows (ws->xe_ref).
+static hd_status denoise_loop(const hd_forward_binding *bw, hd_forward_workspace *ws, int sampler,
+                              const hd_scheduler *sched, int steps, int B, const int64_t *ids,
+                              int T, const float *pos, int ar_len, const void *mask,
+                              const hd_visual_cond *vis, void *z, int I_t, const void *ref,
+                              int n_ref, float guidance, uint64_t seed, float sn_start,
+                              float sn_end, float clip, int S, int H, int KV, int HID, int FF,
+                              int D, int tms, void *scratch, int64_t scratch_bytes, void *stream) {
+    const int I = I_t + n_ref;
     if (steps > sched->num_steps - 1) {
         hd_set_error("denoise: %d steps but the schedule has %d sigmas", steps, sched->num_steps);
         return HD_ERR_UNSUPPORTED;
@@ -611,9 +609,9 @@ extern "C" hd_status hd_denoise(const hd_forward_binding *bw, hd_forward_workspa
         hd_set_error("denoise: scratch too small");
         return HD_ERR_OOM;
     }
-    const int64_t n = (int64_t)I * 3072;
+    const int64_t n = (int64_t)I_t * 3072;
     char *p = (char *)scratch;
-    uint16_t *vin = (uint16_t *)p; p += al256((int64_t)B * n * 2);
+    uint16_t *vin = (uint16_t *)p; p += al256((int64_t)B * I * 3072 * 2);
     uint16_t *xp = (uint16_t *)p; p += al256((int64_t)B * S * 3072 * 2);
     float *mo_c = (float *)p, *mo_u = mo_c + n, *mo = mo_u + n; p += al256(3 * n * 4);
     float *st = (float *)p; p += al256(7 * n * 4);
@@ -637,6 +635,12 @@ extern "C" hd_status hd_denoise(const hd_forward_binding *bw, hd_forward_workspa
     hipStream_t hs = (hipStream_t)hd_hip_get_stream();
     hd_status status = HD_OK;
     for (int i = 0; i < steps; i++) hd_fill_f32(tdev + (size_t)B * i, 1.0f - sched->sigmas[i], B);
+    // reference patches stay put behind the target rows for every step
+    if (ref && hipMemcpyAsync(vin + n, ref, (size_t)n_ref * 3072 * 2, hipMemcpyDeviceToDevice, hs) !=
+                   hipSuccess) {
+        hd_set_error("denoise: reference copy failed");
+        status = HD_ERR_IO;
+    }
 
     // UniPC state: converted outputs rotate through three slots
     float *zf = st, *slot[3] = {st + n, st + 2 * n, st + 3 * n};
@@ -648,7 +652,13 @@ extern "C" hd_status hd_denoise(const hd_forward_binding *bw, hd_forward_workspa
         const float sig = sched->sigmas[i];
         const float sg = sig < kTEps ? kTEps : sig;
         const void *vptr = z;
-        if (B == 2) {
+        if (ref) {
+            if (hipMemcpyAsync(vin, z, n * 2, hipMemcpyDeviceToDevice, hs) != hipSuccess) {
+                hd_set_error("denoise: latent copy failed");
+                status = HD_ERR_IO;
+            }
+            vptr = vin;
+        } else if (B == 2) {
             for (int b = 0; b < 2 && status == HD_OK; b++)
                 if (hipMemcpyAsync(vin + b * n, z, n * 2, hipMemcpyDeviceToDevice, hs) != hipSuccess) {
                     hd_set_error("denoise: latent copy failed");
@@ -657,8 +667,13 @@ extern "C" hd_status hd_denoise(const hd_forward_binding *bw, hd_forward_workspa
             vptr = vin;
         }
         if (status != HD_OK) break;
-        status = hd_forward_batched(bw, ws, B, ids, T, pos, ar_len, vptr, I, tdev + (size_t)B * i,
-                                    S, H, KV, HID, FF, D, tms, nullptr, xp, nullptr);
+        if (B == 1 && (vis || mask || n_ref))
+            status = hd_forward(bw, ws, ids, T, pos, mask, vptr, I, vis, tdev + i, nullptr, S, H, KV,
+                                HID, FF, D, tms, nullptr, xp, nullptr);
+        else
+            status = hd_forward_batched(bw, ws, B, ids, T, pos, ar_len, vptr, I,
+                                        tdev + (size_t)B * i, S, H, KV, HID, FF, D, tms, nullptr, xp,
+                                        nullptr);
         if (status != HD_OK) break;
         hd_cuda_clear_error();
         hd_sched_vcond(z, xp + (size_t)T * 3072, sg, mo_c, (int)n);
@@ -727,4 +742,61 @@ extern "C" hd_status hd_denoise(const hd_forward_binding *bw, hd_forward_workspa
     }
     hd_hip_set_stream(prev_stream);
     return status;
+}
+
+extern "C" hd_status hd_denoise(const hd_forward_binding *bw, hd_forward_workspace *ws, int sampler,
+                                const hd_scheduler *sched, int steps, int B, const int64_t *ids,
+                                int T, const float *pos, int ar_len, void *z, int I,
+                                float guidance, uint64_t seed, float sn_start, float sn_end,
+                                float clip, int S, int H, int KV, int HID, int FF, int D, int tms,
+                                void *scratch, int64_t scratch_bytes, void *stream) {
+    if (!bw || !ws || !sched || !ids || !pos || !z || !scratch || I <= 0 || steps < 1) {
+        hd_set_error("denoise: null argument");
+        return HD_ERR_MISSING;
+    }
+    if ((B != 1 && B != 2) || sampler < HD_SAMPLER_EULER || sampler > HD_SAMPLER_UNIPC) {
+        hd_set_error("denoise: batch must be 1 or 2 and sampler 0..2");
+        return HD_ERR_UNSUPPORTED;
+    }
+    return denoise_loop(bw, ws, sampler, sched, steps, B, ids, T, pos, ar_len, nullptr, nullptr, z,
+                        I, nullptr, 0, guidance, seed, sn_start, sn_end, clip, S, H, KV, HID, FF, D,
+                        tms, scratch, scratch_bytes, stream);
+}
+
+extern "C" hd_status hd_denoise_visual(const hd_forward_binding *bw, hd_forward_workspace *ws,
+                                       int sampler, const hd_scheduler *sched, int steps,
+                                       const int64_t *ids, int T, const float *pos,
+                                       const void *mask, const hd_visual_cond *visual, void *z,
+                                       int img_tokens, const void *ref_patches, int ref_tokens,
+                                       uint64_t seed, float sn_start, float sn_end, float clip,
+                                       int S, int H, int KV, int HID, int FF, int D, int tms,
+                                       void *scratch, int64_t scratch_bytes, void *stream) {
+    if (!bw || !ws || !sched || (!ids && T > 0) || !pos || !z || !scratch || img_tokens <= 0 ||
+        steps < 1 || ref_tokens < 0) {
+        hd_set_error("denoise: null argument");
+        return HD_ERR_MISSING;
+    }
+    if (sampler < HD_SAMPLER_EULER || sampler > HD_SAMPLER_UNIPC) {
+        hd_set_error("denoise: sampler must be 0..2");
+        return HD_ERR_UNSUPPORTED;
+    }
+    if (T + img_tokens + ref_tokens != S) {
+        hd_set_error("denoise: text + target + reference tokens != seq");
+        return HD_ERR_MISMATCH;
+    }
+    // a workspace x_embedder cache stands in for the references' patches
+    // (forward.c:301-313), so it must describe exactly these references
+    const bool cached = ws->xe_ref && ws->n_ref > 0;
+    if (cached && ws->n_ref != ref_tokens) {
+        hd_set_error("denoise: workspace caches %d reference rows, call has %d", ws->n_ref,
+                     ref_tokens);
+        return HD_ERR_MISMATCH;
+    }
+    if (ref_tokens > 0 && !ref_patches && !cached) {
+        hd_set_error("denoise: %d reference tokens without patches or a cache", ref_tokens);
+        return HD_ERR_MISSING;
+    }
+    return denoise_loop(bw, ws, sampler, sched, steps, 1, ids, T, pos, 0, mask, visual, z,
+                        img_tokens, cached ? nullptr : ref_patches, ref_tokens, 0.0f, seed, sn_start, sn_end, clip,
+                        S, H, KV, HID, FF, D, tms, scratch, scratch_bytes, stream);
 }

@@ -326,6 +326,11 @@ SIGNATURES = {
                            ctypes.POINTER(hd_scheduler), c_int, c_int, P, c_int, P, c_int, P, c_int,
                            c_float, ctypes.c_uint64, c_float, c_float, c_float, c_int, c_int, c_int,
                            c_int, c_int, c_int, c_int, P, c_int64, P]),
+    "hd_denoise_visual": (c_int, [ctypes.POINTER(hd_forward_binding), ctypes.POINTER(hd_forward_workspace),
+                                  c_int, ctypes.POINTER(hd_scheduler), c_int, P, c_int, P, P,
+                                  ctypes.POINTER(hd_visual_cond), P, c_int, P, c_int, ctypes.c_uint64,
+                                  c_float, c_float, c_float, c_int, c_int, c_int, c_int, c_int, c_int,
+                                  c_int, P, c_int64, P]),
     "hd_unipc_convert": (None, [P, P, c_float, P, c_int]),
     "hd_unipc_correct": (None, [P, P, P, P] + [c_float] * 8 + [c_int, P, c_int]),
     # hd_sequence.h

@@ -81,3 +81,66 @@ def ulp_diff_bf16(a, b):
     ia = np.where(ia < 0, -(ia & 0x7FFF), ia)
     ib = np.where(ib < 0, -(ib & 0x7FFF), ib)
     return int(np.max(np.abs(ia.astype(np.int64) - ib.astype(np.int64)))) if ia.size else 0
+
+
+class Stepper:
+    """One sampler step composed from the library's own calls, as the
+    reference's step loops run it (generate.c:855-935, :1314-1455):
+    Euler = hd_sched_flow_match_step; flash = host noise from seed + 1
+    clipped at `clip` std, then hd_scheduler_step with the ramped s_noise;
+    UniPC = the per-step plan and the hd_unipc_* kernels over a three-slot
+    history. `step(i, z, m)` updates the bf16 latent z in place from the
+    velocity m (fp32, n values)."""
+
+    def __init__(self, pkg, lib, dev, sampler, sch, n, seed, clip=8.0, sn=(8.0, 8.0)):
+        import ctypes
+        self.pkg, self.lib, self.dev, self.sampler, self.sch, self.n = pkg, lib, dev, sampler, sch, n
+        self.clip, self.sn = clip, sn
+        self.sig = [sch.sigmas[i] for i in range(sch.num_steps)]
+        self.rng = pkg.hd_torch_rng()
+        lib.hd_torch_rng_seed(ctypes.byref(self.rng), seed + 1)
+        self.fs = pkg.hd_scheduler()
+        ctypes.memmove(ctypes.byref(self.fs), ctypes.byref(sch), ctypes.sizeof(sch))
+        f = dict(dtype=torch.float32, device=dev)
+        self.zf, self.corr_b, self.last, self.pred = (torch.empty(n, **f) for _ in range(4))
+        self.slots = [torch.empty(n, **f) for _ in range(3)]
+        self.this_order = self.lower = self.have = 0
+        self.sscr = torch.empty(3 * n, **f)
+
+    def step(self, i, zr, m):
+        import ctypes
+        pkg, lib, n, sig = self.pkg, self.lib, self.n, self.sig
+        if self.sampler == 0:
+            lib.hd_sched_flow_match_step(pkg.ptr(zr), pkg.ptr(m), sig[i], sig[i + 1], pkg.ptr(zr), n)
+        elif self.sampler == 1:
+            noise = np.empty(n, np.float32)
+            lib.hd_step_noise(ctypes.byref(self.rng), pkg.np_ptr(noise), n, self.clip)
+            nd = torch.from_numpy(noise).to(self.dev)
+            self.fs.step_index = i
+            sn = lib.hd_scheduler_noise_scale(ctypes.byref(self.sch), i, self.sn[0], self.sn[1])
+            st = lib.hd_scheduler_step(ctypes.byref(self.fs), pkg.ptr(zr), pkg.ptr(m), pkg.ptr(nd), sn,
+                                       pkg.ptr(zr), n, pkg.ptr(self.sscr))
+            pkg.check_status(st, "scheduler step")
+        else:
+            pl = pkg.hd_unipc_plan()
+            lib.hd_scheduler_unipc_plan(ctypes.byref(self.sch), i, self.this_order, self.lower,
+                                        ctypes.byref(pl))
+            lib.hd_sched_bf16_upcast(pkg.ptr(zr), pkg.ptr(self.zf), n)
+            slots = self.slots
+            cur = slots[0]
+            lib.hd_unipc_convert(pkg.ptr(self.zf), pkg.ptr(m), sig[i], pkg.ptr(cur), n)
+            corr = self.zf
+            if i > 0 and self.this_order > 0 and self.have:
+                lib.hd_unipc_correct(pkg.ptr(self.last), pkg.ptr(slots[1]), pkg.ptr(slots[2]), pkg.ptr(cur),
+                                     pl.c_sig_t, pl.c_sig_s0, pl.c_alpha_t, pl.c_h_phi_1, pl.c_B_h,
+                                     pl.c_rhos0, pl.c_rhos1, pl.c_inv_rks0, pl.corr_order,
+                                     pkg.ptr(self.corr_b), n)
+                corr = self.corr_b
+            self.last.copy_(corr)
+            lib.hd_unipc_predict(pkg.ptr(corr), pkg.ptr(cur), pkg.ptr(slots[1]), pl.p_sig_t, pl.p_sig_s0,
+                                 pl.p_alpha_t, pl.p_h_phi_1, pl.p_B_h, pl.p_rhos_p, pl.p_inv_rks0,
+                                 pl.pred_order, pkg.ptr(self.pred), n)
+            lib.hd_f32_convert_bf16(pkg.ptr(self.pred), pkg.ptr(zr), n)
+            self.slots = [slots[2], slots[0], slots[1]]
+            self.this_order, self.lower, self.have = pl.next_this_order, pl.next_lower_order, 1
+        pkg.check_prim("step %d" % i)

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from oracle import oracle as orc
-from tests.common import make_block_weights, rel_l2, cosine, grid_pos, bf16
+from tests.common import make_block_weights, rel_l2, cosine, grid_pos, bf16, Stepper
 
 pytestmark = pytest.mark.gpu
 
@@ -300,14 +300,7 @@ def test_denoise_samplers_match_stepwise(pkg, lib, dev, sampler, batch):
     mo_c = torch.empty(n, dtype=torch.float32, device=dev)
     mo_u = torch.empty_like(mo_c)
     mo = torch.empty_like(mo_c)
-    rng = pkg.hd_torch_rng()
-    lib.hd_torch_rng_seed(ctypes.byref(rng), seed + 1)
-    fs = pkg.hd_scheduler()
-    ctypes.memmove(ctypes.byref(fs), ctypes.byref(sch), ctypes.sizeof(sch))
-    zf, corr_b, last, pred = (torch.empty_like(mo_c) for _ in range(4))
-    slots = [torch.empty_like(mo_c) for _ in range(3)]
-    this_order = lower = have = 0
-    sscr = torch.empty(3 * n, dtype=torch.float32, device=dev)
+    stepper = Stepper(pkg, lib, dev, sampler, sch, n, seed)
     for i in range(steps):
         s_i = np.float32(sig[i])
         vin = zr.unsqueeze(0).repeat(batch, 1, 1).contiguous()
@@ -323,37 +316,6 @@ def test_denoise_samplers_match_stepwise(pkg, lib, dev, sampler, batch):
             lib.hd_sched_vcond(pkg.ptr(zr), pkg.ptr(out[1, T:]), sg, pkg.ptr(mo_u), n)
             lib.hd_sched_cfg_guided(pkg.ptr(mo_c), pkg.ptr(mo_u), guidance, pkg.ptr(mo), n)
             m = mo
-        if sampler == 0:
-            lib.hd_sched_flow_match_step(pkg.ptr(zr), pkg.ptr(m), sig[i], sig[i + 1], pkg.ptr(zr), n)
-        elif sampler == 1:
-            noise = np.empty(n, np.float32)
-            lib.hd_step_noise(ctypes.byref(rng), pkg.np_ptr(noise), n, 8.0)
-            nd = torch.from_numpy(noise).to(dev)
-            fs.step_index = i
-            sn = lib.hd_scheduler_noise_scale(ctypes.byref(sch), i, 8.0, 8.0)
-            st = lib.hd_scheduler_step(ctypes.byref(fs), pkg.ptr(zr), pkg.ptr(m), pkg.ptr(nd), sn,
-                                       pkg.ptr(zr), n, pkg.ptr(sscr))
-            pkg.check_status(st, "scheduler step")
-        else:
-            pl = pkg.hd_unipc_plan()
-            lib.hd_scheduler_unipc_plan(ctypes.byref(sch), i, this_order, lower, ctypes.byref(pl))
-            lib.hd_sched_bf16_upcast(pkg.ptr(zr), pkg.ptr(zf), n)
-            cur = slots[0]
-            lib.hd_unipc_convert(pkg.ptr(zf), pkg.ptr(m), sig[i], pkg.ptr(cur), n)
-            corr = zf
-            if i > 0 and this_order > 0 and have:
-                lib.hd_unipc_correct(pkg.ptr(last), pkg.ptr(slots[1]), pkg.ptr(slots[2]), pkg.ptr(cur),
-                                     pl.c_sig_t, pl.c_sig_s0, pl.c_alpha_t, pl.c_h_phi_1, pl.c_B_h,
-                                     pl.c_rhos0, pl.c_rhos1, pl.c_inv_rks0, pl.corr_order,
-                                     pkg.ptr(corr_b), n)
-                corr = corr_b
-            last.copy_(corr)
-            lib.hd_unipc_predict(pkg.ptr(corr), pkg.ptr(cur), pkg.ptr(slots[1]), pl.p_sig_t, pl.p_sig_s0,
-                                 pl.p_alpha_t, pl.p_h_phi_1, pl.p_B_h, pl.p_rhos_p, pl.p_inv_rks0,
-                                 pl.pred_order, pkg.ptr(pred), n)
-            lib.hd_f32_convert_bf16(pkg.ptr(pred), pkg.ptr(zr), n)
-            slots = [slots[2], slots[0], slots[1]]
-            this_order, lower, have = pl.next_this_order, pl.next_lower_order, 1
-        pkg.check_prim("step %d" % i)
+        stepper.step(i, zr, m)
     torch.cuda.synchronize()
     assert torch.equal(z, zr)
