@@ -123,8 +123,10 @@ int hd_linear_qkv_rope_ws(const void *x, const void *wq, const void *wk, const v
                           float eps, void *ws, int64_t ws_bytes);
 
 /* Diagnostics/tuning: kernel family for the production GEMMs. 0 (default):
- * 4-wave fragment-ring tiles for K <= 8192, 8-wave interleaved tiles above;
- * 1: 8-wave interleaved tiles for every shape. Returns the previous value. */
+ * 8-wave fragment-ring tiles with buffer loads for every K (the fused QKV
+ * epilogue included); 1: the previous kernels, 4-wave fragment-ring tiles
+ * for K <= 8192 and 8-wave interleaved tiles above. Both compute identical
+ * values. Returns the previous value. */
 int hd_gemm_set_family(int family);
 
 #ifdef __cplusplus

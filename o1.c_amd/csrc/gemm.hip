@@ -780,8 +780,13 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
     }
     __syncthreads();   // every wave is done with the ring before staging reuses it
 
-    constexpr int WO = C::WTN_OUT, LDW = WO + C::EPAD;
-    uint16_t *stg = smem + wave * WTM * LDW;
+    // QKV with 64-wide wave tiles (8 waves): the two waves of one 128-wide
+    // head stage into one [WTM][128 + pad] area, side by side
+    constexpr bool QHALF = EPI == EPI_QKV && WTN == 64;
+    static_assert(EPI != EPI_QKV || WTN == 128 || WTN == 64, "QKV epilogue: 64- or 128-wide wave tiles");
+    constexpr int WO = C::WTN_OUT, LDW = QHALF ? 128 + C::EPAD : WO + C::EPAD;
+    uint16_t *const hstg = smem + (wm * (WGN / 2) + wn / 2) * WTM * LDW;   // QHALF: the head's area
+    uint16_t *stg = QHALF ? hstg + (wn % 2) * 64 : smem + wave * WTM * LDW;
     // a lane holds, per accumulator, runs of 4 consecutive output columns:
     // 32x32: columns q*8 + khalf*4 (q < 4) of row lane % 32;
     // 16x16: columns (lane / 16)*4 of row lane % 16
@@ -815,7 +820,12 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
     constexpr int CPRO = WO / 8, RPIO = 64 / CPRO;
     const int gm0 = m0 + wm * WTM;
     const int gn0 = tn * C::BN_OUT + wn * WO;
-    if constexpr (EPI == EPI_QKV) {
+    if constexpr (QHALF) {
+        // each of the head's two waves finishes half of its rows
+        const int hr = (wn % 2) * (WTM / 2);
+        qkv_epilogue<WTM / 2, LDW>(g, hstg + hr * LDW, gm0 + hr, gn0 / 128, lane);
+        return;
+    } else if constexpr (EPI == EPI_QKV) {
         qkv_epilogue<WTM, LDW>(g, stg, gm0, gn0 / 128, lane);
         return;
     }
@@ -1295,6 +1305,8 @@ static bool run_table(int cfg, GemmArgs &g) {
     case 42: launch_ms<256, 256, 32, 4, 2, 2, EPI, 3, 1, 5>(g); return true;
     case 43: launch_ms<192, 256, 32, 4, 2, 2, EPI, 3, 1, 5>(g); return true;
     case 44: launch_ms<256, 256, 32, 3, 2, 2, EPI, 3, 1, 5>(g); return true;
+    case 50: launch_ms<256, 256, 64, 2, 2, 4, EPI, 3, 1, 5>(g); return true;  // 8-wave ring, buffer loads
+    case 51: launch_ms<192, 256, 64, 2, 2, 4, EPI, 3, 1, 5>(g); return true;
     case 7: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 1>(g); return true;    // diag: compute only
     case 8: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 2>(g); return true;    // diag: loads only
     default: return false;
@@ -1358,31 +1370,50 @@ static const char *pick_and_launch(GemmArgs &g, bool launch, void *ws = nullptr,
         if (launch) launch_ms<128, 128, 64, 2, 2, 2, EPI, 1, 2>(g, ws, ws_bytes);
         return p128 > 1 ? "bf16_128x128x64_w2x2_occ2_split" : "bf16_128x128x64_w2x2_occ2";
     }
-    // K <= 8192: 4 waves of 128x128 with one fragment ring across the K loop;
-    // deeper K: 8 interleaved waves. Operands through buffer loads straight
-    // to LDS when each is under 2 GiB (32-bit byte offsets).
+    // Family 0 (production): 8 waves (2 x 4) of 128x64 with one fragment
+    // ring across the K loop and buffer loads straight to LDS (each operand
+    // under 2 GiB: 32-bit byte offsets); two waves per SIMD cover each
+    // other's barrier and load-issue stalls. Family 1 (the previous
+    // kernels, kept for same-process comparisons): 4 waves of 128x128 for
+    // K <= 8192, 8 interleaved waves for deeper K.
     const bool fits = (size_t)(g.M + 256) * g.K * 2 < ((size_t)1 << 31) &&
                       (size_t)g.N * g.K * 2 < ((size_t)1 << 31);
-    const bool ring = g_family == 0 && g.K <= 8192 && fits;
     const bool use192 = c192 < c256;
+    const bool split256 = p256 > 1;
+    if (g_family == 0) {
+        if (use192) {
+            if (fits) {
+                if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 3, 1, 5>(g, ws, ws_bytes);
+                return "bf16_192x256x64_w2x4_ring_buf";
+            }
+            if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 3>(g, ws, ws_bytes);
+            return "bf16_192x256x64_w2x4_ring";
+        }
+        if (fits) {
+            if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 3, 1, 5>(g, ws, ws_bytes);
+            return split256 ? "bf16_256x256x64_w2x4_ring_buf_tailsplit" : "bf16_256x256x64_w2x4_ring_buf";
+        }
+        if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 3>(g, ws, ws_bytes);
+        return split256 ? "bf16_256x256x64_w2x4_ring_tailsplit" : "bf16_256x256x64_w2x4_ring";
+    }
+    const bool ring4 = g.K <= 8192 && fits;
     if (use192) {
-        if (ring) {
+        if (ring4) {
             if (launch) launch_ms<192, 256, 64, 2, 2, 2, EPI, 3, 1, 5>(g, ws, ws_bytes);
             return "bf16_192x256x64_w2x2_ring_buf";
         }
-        if (fits && g_family == 0) {
+        if (fits) {
             if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 1, 1, 5>(g, ws, ws_bytes);
             return "bf16_192x256x64_w2x4_ilv_buf";
         }
         if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 1>(g, ws, ws_bytes);
         return "bf16_192x256x64_w2x4_ilv";
     }
-    const bool split256 = p256 > 1;
-    if (ring) {
+    if (ring4) {
         if (launch) launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 5>(g, ws, ws_bytes);
         return split256 ? "bf16_256x256x64_w2x2_ring_buf_tailsplit" : "bf16_256x256x64_w2x2_ring_buf";
     }
-    if (fits && g_family == 0) {
+    if (fits) {
         if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 1, 1, 5>(g, ws, ws_bytes);
         return split256 ? "bf16_256x256x64_w2x4_ilv_buf_tailsplit" : "bf16_256x256x64_w2x4_ilv_buf";
     }
@@ -1415,7 +1446,7 @@ extern "C" int hd_linear_qkv_rope_ws(const void *x, const void *wq, const void *
         seq <= 0 || heads <= 0 || kv_heads <= 0 || hidden <= 0)
         return 1;
     const int M = batch * seq, N = (heads + 2 * kv_heads) * 128;
-    const bool ok = g_family == 0 && seq % 64 == 0 && (heads * 128) % 256 == 0 &&
+    const bool ok = seq % 64 == 0 && (heads * 128) % 256 == 0 &&
                     (kv_heads * 128) % 256 == 0 && hidden % 64 == 0 && hidden <= 8192 &&
                     (size_t)(M + 256) * hidden * 2 < ((size_t)1 << 31) &&
                     (size_t)heads * 128 * hidden * 2 < ((size_t)1 << 31) &&
@@ -1442,10 +1473,14 @@ extern "C" int hd_linear_qkv_rope_ws(const void *x, const void *wq, const void *
     if (ws && (uintptr_t)ws % 16) ws = nullptr;
     const bool split256 =
         ws && tail_split_of(t256, hidden / 64, (size_t)256 * 256 * 4, ws_bytes, (size_t)256 * 256 * 2) > 1;
-    if (!split256 && quant_eff(t192) > quant_eff(t256) * 1.12)
-        launch_ms<192, 256, 64, 2, 2, 2, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
-    else
-        launch_ms<256, 256, 64, 2, 2, 2, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
+    const bool use192 = !split256 && quant_eff(t192) > quant_eff(t256) * 1.12;
+    if (g_family == 0) {   // 8 waves: two 64-wide wave tiles per head
+        if (use192) launch_ms<192, 256, 64, 2, 2, 4, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
+        else launch_ms<256, 256, 64, 2, 2, 4, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
+    } else {
+        if (use192) launch_ms<192, 256, 64, 2, 2, 2, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
+        else launch_ms<256, 256, 64, 2, 2, 2, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
+    }
     hd_check_launch("linear_qkv_rope");
     return 0;
 }

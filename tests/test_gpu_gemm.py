@@ -118,3 +118,75 @@ def test_linear_reference_backend(pkg, lib, dev):
     torch.cuda.synchronize()
     ref = (x.float() @ w.float().t()).to(torch.bfloat16).float()
     assert close_bf16(y.float().cpu().numpy(), ref.cpu().numpy(), ulps=1)
+
+
+@pytest.mark.parametrize("M", [1152, 8704, 700])
+def test_gemm_families_identical(pkg, lib, dev, M):
+    """The production GEMM family (8-wave fragment ring, buffer loads) and the
+    previous one (4-wave ring / 8-wave interleaved) sum every output in the
+    same K order: plain, residual, SwiGLU and the fused QKV epilogue must
+    agree bit for bit (M = 700 exercises partial row tiles)."""
+    g = torch.Generator(device=dev).manual_seed(M)
+    K, N, F = 1024, 2048, 1536
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    wd = (torch.randn(N, 3 * K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    xd = torch.randn(M, 3 * K, generator=g, device=dev).to(torch.bfloat16)
+    wg = (torch.randn(F, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    wu = (torch.randn(F, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    r = torch.randn(M, N, generator=g, device=dev).to(torch.bfloat16)
+    outs = []
+    prev = lib.hd_gemm_set_family(0)
+    try:
+        for fam in (0, 1):
+            lib.hd_gemm_set_family(fam)
+            y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+            yr = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+            ys = torch.empty(M, F, dtype=torch.bfloat16, device=dev)
+            lib.hd_linear(pkg.ptr(x), pkg.ptr(w), None, pkg.ptr(y), M, N, K, 1)
+            lib.hd_linear_residual(pkg.ptr(xd), pkg.ptr(wd), pkg.ptr(r), pkg.ptr(yr), M, N, 3 * K)
+            lib.hd_linear_swiglu(pkg.ptr(x), pkg.ptr(wg), pkg.ptr(wu), pkg.ptr(ys), M, F, K)
+            pkg.check_prim("gemm family %d" % fam)
+            torch.cuda.synchronize()
+            outs.append((y, yr, ys))
+    finally:
+        lib.hd_gemm_set_family(prev)
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    assert float(outs[0][2].float().abs().mean()) > 0
+
+
+def test_qkv_rope_families_identical(pkg, lib, dev):
+    """Fused QKV epilogue: 8-wave tiles (two waves per head, each finishing
+    half the rows) equal the 4-wave tiles (one head per wave) bit for bit."""
+    B, S, H, KV, HID, D = 2, 1152, 8, 2, 1024, 128
+    g = torch.Generator(device=dev).manual_seed(11)
+    x = torch.randn(B * S, HID, generator=g, device=dev).to(torch.bfloat16)
+    wq = (torch.randn(H * D, HID, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    wk = (torch.randn(KV * D, HID, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    wv = (torch.randn(KV * D, HID, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    qn = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    kn = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    pos = torch.zeros(3, S, dtype=torch.float32)
+    pos[1] = torch.arange(S) // 32
+    pos[2] = torch.arange(S) % 32
+    cs = pkg.rope_table(pos.to(dev), S, D, theta=1e4)
+    outs = []
+    prev = lib.hd_gemm_set_family(0)
+    try:
+        for fam in (0, 1):
+            lib.hd_gemm_set_family(fam)
+            q = torch.zeros(B, H, S, D, dtype=torch.bfloat16, device=dev)
+            k = torch.zeros(B, KV, S, D, dtype=torch.bfloat16, device=dev)
+            vt = torch.zeros(B, KV, D, S, dtype=torch.bfloat16, device=dev)
+            assert lib.hd_linear_qkv_rope(pkg.ptr(x), pkg.ptr(wq), pkg.ptr(wk), pkg.ptr(wv), pkg.ptr(qn),
+                                          pkg.ptr(kn), pkg.ptr(cs), pkg.ptr(q), pkg.ptr(k), pkg.ptr(vt),
+                                          B, S, H, KV, HID, 1e-6) == 0
+            pkg.check_prim("qkv family %d" % fam)
+            torch.cuda.synchronize()
+            outs.append((q, k, vt))
+    finally:
+        lib.hd_gemm_set_family(prev)
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    assert float(outs[0][0].float().abs().mean()) > 0.1
