@@ -84,8 +84,11 @@ __device__ __forceinline__ float xor32_sum(float v) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <bool MASKED>
-__global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
+// NWV waves per block (4: two blocks per CU; 8: one block of 256 queries
+// per CU sharing one copy of the K / V^T tiles); 32 queries per wave either way.
+template <bool MASKED, int NWV>
+__global__ __launch_bounds__(NWV * 64, 8 / NWV) void flash_fwd_kernel(FaArgs a) {
+    constexpr int BQ = NWV * 32, LPW = 16 / NWV;   // queries per block, loads per wave per tile
     __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * (FA_BK * FA_D + FA_D * FA_BK)];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -93,7 +96,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
 
     // block -> (b, head, q tile). Query heads sharing one kv head get
     // consecutive linear ids so they run close together in time.
-    const int nqt = (a.q_row_end + FA_BQ - 1) / FA_BQ;
+    const int nqt = (a.q_row_end + BQ - 1) / BQ;
     const int group = a.Hq / a.Hkv;
     int lin = blockIdx.x, chunk = -1, item = 0;
     if (lin >= a.n_whole) {
@@ -107,13 +110,13 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
     const int b = lin / a.Hkv;
     const int hq = hk * group + g;
 
-    const int q0 = qt * FA_BQ + wave * 32;
+    const int q0 = qt * BQ + wave * 32;
     const int my_q = q0 + l32;                       // this lane's query row
-    const bool causal_block = (qt * FA_BQ) < a.ar_len;
+    const bool causal_block = (qt * BQ) < a.ar_len;
     // keys needed by this block
     int kv_end = a.S;
     if (causal_block) {
-        int last_row = min(qt * FA_BQ + FA_BQ, a.q_row_end) - 1;
+        int last_row = min(qt * BQ + BQ, a.q_row_end) - 1;
         if (last_row < a.ar_len) kv_end = last_row + 1;
     }
     int t_begin = 0, t_end = (kv_end + FA_BK - 1) / FA_BK;
@@ -144,24 +147,24 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
     // as zero (their scores are masked: S % 64 != 0 selects the masked
     // kernel), V^T columns are zero-padded to S_pad
     const int kbytes = a.S * FA_D * 2, vbytes = FA_D * a.S_pad * 2;
-    uint32_t k_vo[4], v_vo[4];
+    uint32_t k_vo[LPW], v_vo[LPW];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int krow = (wave * 4 + i) * 4 + (lane >> 4);
+    for (int i = 0; i < LPW; i++) {
+        const int krow = (wave * LPW + i) * 4 + (lane >> 4);
         k_vo[i] = (uint32_t)(krow * FA_D + (((lane & 15) ^ (krow & 15)) * 8)) * 2;
-        const int vrow = (wave * 4 + i) * 8 + (lane >> 3);
+        const int vrow = (wave * LPW + i) * 8 + (lane >> 3);
         v_vo[i] = (uint32_t)(vrow * a.S_pad + (((lane & 7) ^ ((vrow >> 1) & 7)) * 8)) * 2;
     }
     auto issue = [&](int t, int buf) {
         uint16_t *Ks = Ks0 + buf * FA_BK * FA_D, *Vs = Vs0 + buf * FA_D * FA_BK;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < LPW; i++)
             fa_buf_load16(kbase, kbytes, k_vo[i], (uint32_t)t * FA_BK * FA_D * 2,
-                          (HD_LDS void *)(Ks + (wave * 4 + i) * 512));
+                          (HD_LDS void *)(Ks + (wave * LPW + i) * 512));
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < LPW; i++)
             fa_buf_load16(vbase, vbytes, v_vo[i], (uint32_t)t * FA_BK * 2,
-                          (HD_LDS void *)(Vs + (wave * 4 + i) * 512));
+                          (HD_LDS void *)(Vs + (wave * LPW + i) * 512));
     };
 
     f32x16_t o[4];
@@ -266,7 +269,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
     const float l_tot = xor32_sum(l_run);
     if (chunk >= 0) {
         // partial: O relative to this chunk's running max, with (m, l)
-        float *po = a.part + ((size_t)item * FA_BQ + wave * 32 + l32) * FA_D;
+        float *po = a.part + ((size_t)item * BQ + wave * 32 + l32) * FA_D;
 #pragma unroll
         for (int dt = 0; dt < 4; dt++)
 #pragma unroll
@@ -276,8 +279,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FaArgs a) {
                                         o[dt][gq * 4 + 3]};
             }
         if (h == 0) {
-            float2 *pml = (float2 *)(a.part + (size_t)(gridDim.x - a.n_whole) * FA_BQ * FA_D);
-            pml[(size_t)item * FA_BQ + wave * 32 + l32] = make_float2(m_run, l_tot);
+            float2 *pml = (float2 *)(a.part + (size_t)(gridDim.x - a.n_whole) * BQ * FA_D);
+            pml[(size_t)item * BQ + wave * 32 + l32] = make_float2(m_run, l_tot);
         }
         return;
     }
@@ -319,27 +322,28 @@ __global__ __launch_bounds__(256) void fa_vt_kernel(const uint16_t *v, uint16_t 
 
 // Merges the tail units' key-chunk partials: O = sum_i w_i O_i / sum_i w_i l_i
 // with w_i = 2^((m_i - max_j m_j) * scale_log2). One thread per (row, d).
+template <int BQ>
 __global__ __launch_bounds__(256) void fa_merge_kernel(FaArgs a, int n_tail) {
     const int idx = blockIdx.x * 256 + threadIdx.x;
-    const int d = idx % FA_D, row = (idx / FA_D) % FA_BQ, tu = idx / (FA_D * FA_BQ);
+    const int d = idx % FA_D, row = (idx / FA_D) % BQ, tu = idx / (FA_D * BQ);
     if (tu >= n_tail) return;
     const int P = a.split, n_items = n_tail * P;
-    const float2 *pml = (const float2 *)(a.part + (size_t)n_items * FA_BQ * FA_D);
+    const float2 *pml = (const float2 *)(a.part + (size_t)n_items * BQ * FA_D);
     float m = -INFINITY;
-    for (int i = 0; i < P; i++) m = fmaxf(m, pml[(size_t)(tu * P + i) * FA_BQ + row].x);
+    for (int i = 0; i < P; i++) m = fmaxf(m, pml[(size_t)(tu * P + i) * BQ + row].x);
     float L = 0.f, acc = 0.f;
     for (int i = 0; i < P; i++) {
-        const float2 ml = pml[(size_t)(tu * P + i) * FA_BQ + row];
+        const float2 ml = pml[(size_t)(tu * P + i) * BQ + row];
         const float w = __builtin_amdgcn_exp2f((ml.x - m) * a.scale_log2);
         L = fmaf(w, ml.y, L);
-        acc = fmaf(w, a.part[((size_t)(tu * P + i) * FA_BQ + row) * FA_D + d], acc);
+        acc = fmaf(w, a.part[((size_t)(tu * P + i) * BQ + row) * FA_D + d], acc);
     }
-    const int nqt = (a.q_row_end + FA_BQ - 1) / FA_BQ, group = a.Hq / a.Hkv;
+    const int nqt = (a.q_row_end + BQ - 1) / BQ, group = a.Hq / a.Hkv;
     int lin = a.n_whole + tu;
     const int g = lin % group; lin /= group;
     const int qt = lin % nqt; lin /= nqt;
     const int hk = lin % a.Hkv, b = lin / a.Hkv, hq = hk * group + g;
-    const int my_q = qt * FA_BQ + row;
+    const int my_q = qt * BQ + row;
     if (my_q >= a.q_row_end) return;
     const size_t o = a.out_seq_major ? (((size_t)b * a.S + my_q) * a.Hq + hq) * FA_D + d
                                      : (((size_t)b * a.Hq + hq) * a.S + my_q) * FA_D + d;
@@ -347,26 +351,39 @@ __global__ __launch_bounds__(256) void fa_merge_kernel(FaArgs a, int n_tail) {
 }
 
 // Resident flash blocks on the current device (occupancy x CUs), cached.
-static int fa_slots() {
-    static int dev_cached = -1, slots = 0;
+static int fa_slots(int nwv = 4) {
+    static int dev_cached = -1, slots4 = 0, slots8 = 0;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
     if (dev != dev_cached) {
-        int per_cu = 0, cus = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, flash_fwd_kernel<false>, 256, 0) !=
+        int per4 = 0, per8 = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per4, flash_fwd_kernel<false, 4>, 256, 0) !=
+                hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per8, flash_fwd_kernel<false, 8>, 512, 0) !=
                 hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             return 0;
-        slots = per_cu * cus;
+        slots4 = per4 * cus;
+        slots8 = per8 * cus;
         dev_cached = dev;
     }
-    return slots;
+    return nwv == 8 ? slots8 : slots4;
+}
+
+// hd_flash_set_family: 0 = automatic (below), 1 = 4-wave blocks, 2 = 8-wave
+static int g_fa_family = 0;
+extern "C" int hd_flash_set_family(int family) {
+    const int prev = g_fa_family;
+    g_fa_family = family == 1 || family == 2 ? family : 0;
+    return prev;
 }
 
 // Workspace for the tail split: at most one round of partial blocks.
 extern "C" int64_t hd_flash_ws_bytes(void) {
-    const int slots = fa_slots();
-    return (int64_t)(slots > 0 ? slots : 1024) * FA_BQ * (FA_D + 2) * 4;
+    // one round of partial blocks of either family (slots x rows per block)
+    const int64_t r4 = (int64_t)fa_slots(4) * 128, r8 = (int64_t)fa_slots(8) * 256;
+    const int64_t rows = r4 > r8 ? r4 : r8;
+    return (rows > 0 ? rows : 1024 * 128) * (FA_D + 2) * 4;
 }
 
 extern "C" int64_t hd_flash_vt_bytes(int batch, int kv_heads, int seq) {
@@ -404,7 +421,14 @@ static int fa_launch(const void *q, const void *k, const void *vt, const void *m
     a.scale_log2 = scale * 1.44269504088896341f;
     a.inv_scale = 1.0f / scale;
     a.out_seq_major = out_seq_major;
-    const int nqt = (q_row_end + FA_BQ - 1) / FA_BQ;
+    // 8-wave blocks (one copy of each K / V^T tile for 256 queries) when the
+    // tail split can fill the last round and the sequence is long enough to
+    // amortise the larger block: +3 % at S = 16640 / 16896, equal at 4352;
+    // 4-wave blocks otherwise (without the split their finer grain wins)
+    const bool split_ok = ws && !mask && ar_len == 0;
+    const int nwv = g_fa_family == 1 ? 4 : g_fa_family == 2 ? 8 : (split_ok && seq >= 1024 ? 8 : 4);
+    const int BQ = nwv * 32;
+    const int nqt = (q_row_end + BQ - 1) / BQ;
     const int units = batch * hq * nqt;
     bool masked = mask || ar_len > 0 || (seq % FA_BK) != 0;
     // Tail split (full attention only): the units of the last partial round
@@ -414,24 +438,30 @@ static int fa_launch(const void *q, const void *k, const void *vt, const void *m
     a.split = 1;
     a.part = (float *)ws;
     int n_tail = 0;
-    const int slots = ws ? fa_slots() : 0;
+    const int slots = ws ? fa_slots(nwv) : 0;
     if (slots > 0 && !mask && ar_len == 0 && units >= slots) {
         const int rem = units % slots, ntile = (seq + FA_BK - 1) / FA_BK;
         int P = rem ? slots / rem : 1;
         if (P > 8) P = 8;
         if (P > ntile) P = ntile;
-        if (rem && P >= 2 && (int64_t)rem * P * FA_BQ * (FA_D + 2) * 4 <= ws_bytes) {
+        if (rem && P >= 2 && (int64_t)rem * P * BQ * (FA_D + 2) * 4 <= ws_bytes) {
             n_tail = rem;
             a.n_whole = units - rem;
             a.split = P;
         }
     }
     dim3 grid((unsigned)(a.n_whole + n_tail * a.split));
-    if (masked) flash_fwd_kernel<true><<<grid, 256, 0, st>>>(a);
-    else flash_fwd_kernel<false><<<grid, 256, 0, st>>>(a);
+    if (nwv == 8) {
+        if (masked) flash_fwd_kernel<true, 8><<<grid, 512, 0, st>>>(a);
+        else flash_fwd_kernel<false, 8><<<grid, 512, 0, st>>>(a);
+    } else {
+        if (masked) flash_fwd_kernel<true, 4><<<grid, 256, 0, st>>>(a);
+        else flash_fwd_kernel<false, 4><<<grid, 256, 0, st>>>(a);
+    }
     if (n_tail) {
-        dim3 gm((unsigned)hd_cdiv((int64_t)n_tail * FA_BQ * FA_D, 256));
-        fa_merge_kernel<<<gm, 256, 0, st>>>(a, n_tail);
+        dim3 gm((unsigned)hd_cdiv((int64_t)n_tail * BQ * FA_D, 256));
+        if (nwv == 8) fa_merge_kernel<256><<<gm, 256, 0, st>>>(a, n_tail);
+        else fa_merge_kernel<128><<<gm, 256, 0, st>>>(a, n_tail);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {

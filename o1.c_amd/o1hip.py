@@ -237,6 +237,7 @@ SIGNATURES = {
     "hd_gemm_config_name": (c_char_p, [c_int, c_int, c_int, c_int]),
     "hd_gemm_tune_run": (c_int, [c_int, c_int, P, P, P, P, c_int, c_int, c_int]),
     "hd_gemm_set_family": (c_int, [c_int]),
+    "hd_flash_set_family": (c_int, [c_int]),
     "hd_linear_qkv_rope": (c_int, [P, P, P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float]),
     "hd_linear_qkv_rope_ws": (c_int, [P] * 10 + [c_int] * 5 + [c_float, P, ctypes.c_int64]),
     # hd_sdpa.h

@@ -372,7 +372,9 @@ def test_flash_tail_split_matches_unsplit(pkg, lib, dev, S, seq_major):
     torch.cuda.synchronize()
     af, bf = a.float(), b.float()
     assert float((af - bf).norm() / af.norm()) < 2e-3
-    assert float((af == bf).float().mean()) > 0.97
+    # with the workspace the 8-wave kernel runs (256 query rows per unit):
+    # 32 of its 32 x 9 units are the split tail, up to 12 % of the rows
+    assert float((af == bf).float().mean()) > 0.9
     assert float((af - bf).abs().max()) <= 4 * 2 ** -8 * float(af.abs().max())
     # the split really ran: the last query tiles of the last heads differ
     # in at least a few bits somewhere, or match exactly when the merge
@@ -486,3 +488,37 @@ def test_swiglu_tail_split(pkg, lib, dev):
     print("identical fraction", same)
     assert same >= 6144 / 6240 - 1e-3 and same < 1.0
     assert float(d.norm() / a.norm()) < 1e-3
+
+
+@pytest.mark.parametrize("S,ar_len,dense", [(2176, 0, False), (1152, 127, False), (1000, 0, False),
+                                            (576, 0, True)])
+def test_flash_families_identical(pkg, lib, dev, S, ar_len, dense):
+    """4-wave blocks (128 queries) and 8-wave blocks (256 queries sharing one
+    copy of each K / V^T tile) run the same per-row arithmetic: full
+    attention, a causal text prefix, S % 64 != 0 and a dense additive mask
+    agree bit for bit."""
+    B, Hq, Hkv, D = 2, 8, 2, 128
+    g = torch.Generator(device=dev).manual_seed(S + ar_len)
+    q = torch.randn(B, Hq, S, D, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, S, D, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(B * Hkv, S, D, generator=g, device=dev).to(torch.bfloat16)
+    vt = torch.empty(lib.hd_flash_vt_bytes(B, Hkv, S) // 2, dtype=torch.bfloat16, device=dev)
+    lib.hd_flash_make_vt(pkg.ptr(v), pkg.ptr(vt), B * Hkv, S)
+    mask = None
+    if dense:
+        mask = (torch.randn(S, S, generator=g, device=dev) * 2).to(torch.bfloat16)
+    outs = []
+    prev = lib.hd_flash_set_family(1)
+    try:
+        for fam in (1, 2):
+            lib.hd_flash_set_family(fam)
+            o = torch.zeros(B, S, Hq * D, dtype=torch.bfloat16, device=dev)
+            assert lib.hd_flash_attention(pkg.ptr(q), pkg.ptr(k), pkg.ptr(vt),
+                                          pkg.ptr(mask) if mask is not None else None, pkg.ptr(o),
+                                          B, Hq, Hkv, S, D, ar_len, D ** -0.5, 1) == 0
+            torch.cuda.synchronize()
+            outs.append(o)
+    finally:
+        lib.hd_flash_set_family(prev)
+    assert torch.equal(outs[0], outs[1])
+    assert float(outs[0].float().abs().sum(dim=-1).min()) > 0
