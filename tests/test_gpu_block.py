@@ -139,3 +139,41 @@ def test_block_config0_full_size(pkg, lib, dev):
     check(got, ref, x.numpy(), "config0 vs fp32")
     reff = oracle_block(w, x.numpy(), pos, H, KV, HID, FF, D, 1e4, faithful=1)
     check(got, reff, x.numpy(), "config0 vs bf16-faithful", rel=5e-3, cos=0.99995, delta=3e-2)
+
+
+def test_block_config1_full_size(pkg, lib, dev):
+    """Benchmark configuration 1's block at its real shape: batch 2 (CFG) x
+    (64x64 image tokens + 256 text) = 2 x 4352 rows through
+    hd_decoder_block_batched, i.e. the production kernels with every tail
+    split active (QKV 816 tiles, o_proj / down 544 tiles, attention 1088
+    256-query units over 256 slots), against the fp32 oracle of both
+    sequences and the bf16-faithful oracle."""
+    H, KV, HID, FF, D = 32, 8, 4096, 12288, 128
+    T, gh, gw, B = 256, 64, 64, 2
+    S = T + gh * gw
+    w = make_block_weights(HID, H, KV, FF, D, seed=10)
+    x = bf16(torch.randn(B * S, HID, generator=torch.Generator().manual_seed(11)))
+    pos = grid_pos(T, gh, gw)
+    pkg.set_block_config(theta=1e4)
+    wd = {k: to_dev(v, dev) for k, v in w.items()}
+    bind = pkg.binding_from(wd)
+    xd = x.to(dev, torch.bfloat16)
+    out = torch.empty_like(xd)
+    posd = torch.from_numpy(pos).to(dev)
+    cs = pkg.rope_table(posd, S, D, theta=1e4)
+    nbytes = lib.hd_decoder_block_batched_scratch_bytes(B, S, H, KV, HID, FF, D)
+    scratch = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    print(f"config1 block B={B} S={S}", flush=True)
+    st = lib.hd_decoder_block_batched(pkg.ptr(xd), pkg.ptr(cs), None, 0, bind, pkg.ptr(scratch),
+                                      nbytes, None, pkg.ptr(out), B, S, H, KV, HID, FF, D)
+    pkg.check_status(st, "batched config1")
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    del wd, bind, xd, out, scratch
+    ref = oracle_block(w, x.numpy(), pos, H, KV, HID, FF, D, 1e4, faithful=0, batch=B)
+    check(got, ref, x.numpy(), "config1 vs fp32")
+    for b in range(B):
+        rows = slice(b * S, (b + 1) * S)
+        check(got[rows], ref[rows], x.numpy()[rows], f"config1 seq {b} vs fp32")
+    reff = oracle_block(w, x.numpy(), pos, H, KV, HID, FF, D, 1e4, faithful=1, batch=B)
+    check(got, reff, x.numpy(), "config1 vs bf16-faithful", rel=5e-3, cos=0.99995, delta=3e-2)
