@@ -63,6 +63,10 @@ def main():
     ap.add_argument("--vision-only", action="store_true",
                     help="run only the vision tower of configuration 3 (3 references of 24x24 "
                          "patches, one multi-image call, 10 untimed + 10 timed), for rocprofv3")
+    ap.add_argument("--elementwise", action="store_true",
+                    help="time each HBM-bound kernel of the path (norms, rotary, QKV epilogue, "
+                         "SwiGLU, residual, head permutes, sampler pointwise, patchify) at "
+                         "configuration 2's sizes and print its HBM rate against 8 TB/s")
     ap.add_argument("--kernel-only", action="store_true",
                     help="run only the dominant kernel (gate/up GEMM + SwiGLU at the step's "
                          "shape) and a 1 GiB device copy, for rocprofv3 counter passes")
@@ -87,6 +91,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.init()
     pkg.bind_torch_stream()
+    if args.elementwise:
+        elementwise_bench(pkg, lib, args.kernel_iters)
+        return
     if args.kernel_only:
         kernel_only(pkg, lib, B * S, args.kernel_iters)
         return
@@ -513,6 +520,77 @@ def kernel_only(pkg, lib, M, iters):
     dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"kernel_only": True, "M": M, "iters": iters, "copy_bytes": 1 << 30}))
+
+
+def elementwise_bench(pkg, lib, iters):
+    """HBM-bound kernels at configuration 2's sizes (S = 16640 rows, hidden
+    4096, FFN 12288; 16384 image tokens x 3072 patch features; a 4096^2 RGB
+    image at 32-px patches), each launched `iters` times between HIP events
+    on the library's stream. Bytes are algorithmic: every operand read once
+    and every result written once."""
+    import torch
+    dev = torch.device("cuda:0")
+    S, I, P = 16640, 16384, 3072
+    g = torch.Generator(device=dev).manual_seed(0)
+    bfr = lambda *sh: torch.randn(*sh, generator=g, device=dev).to(torch.bfloat16)
+    f32 = lambda *sh: torch.randn(*sh, generator=g, device=dev)
+    x, a, y, sm = bfr(S, HID), bfr(S, HID), torch.empty(S, HID, dtype=torch.bfloat16, device=dev), \
+        torch.empty(S, HID, dtype=torch.bfloat16, device=dev)
+    w = bfr(HID)
+    gt, up, sw = bfr(S, FF), bfr(S, FF), torch.empty(S, FF, dtype=torch.bfloat16, device=dev)
+    qkv = bfr(S, (NH + 2 * NKV) * D)
+    qn, kn = bfr(D), bfr(D)
+    pos = torch.zeros(3, S, device=dev)
+    cs = pkg.rope_table(pos, S, D, theta=1e4)
+    q, k = torch.empty(NH, S, D, dtype=torch.bfloat16, device=dev), torch.empty(NKV, S, D, dtype=torch.bfloat16, device=dev)
+    vt = torch.empty(NKV, D, S, dtype=torch.bfloat16, device=dev)
+    qh, qo = bfr(NH, S, D), torch.empty(NH, S, D, dtype=torch.bfloat16, device=dev)
+    cc, ss = f32(S, D), f32(S, D)
+    hs = torch.empty(S, NH * D, dtype=torch.bfloat16, device=dev)
+    z, xp = bfr(I * P), bfr(I * P)
+    mo, mu, mg = f32(I * P), f32(I * P), torch.empty(I * P, device=dev)
+    zn = torch.empty(I * P, dtype=torch.bfloat16, device=dev)
+    img, tok = f32(3, 128 * 32, 128 * 32), torch.empty(I, P, dtype=torch.bfloat16, device=dev)
+    pt = pkg.ptr
+    E = S * HID
+    cases = [
+        ("rmsnorm [16640 x 4096]", 4 * E, lambda: lib.hd_rmsnorm(pt(x), pt(w), pt(y), S, HID, 1e-6)),
+        ("add_rmsnorm [16640 x 4096] (sum and norm out)", 8 * E,
+         lambda: lib.hd_add_rmsnorm(pt(x), pt(a), pt(w), pt(sm), pt(y), S, HID, 1e-6)),
+        ("residual_add [16640 x 4096]", 6 * E, lambda: lib.hd_residual_add(pt(x), pt(a), pt(y), E)),
+        ("swiglu [16640 x 12288]", 6 * S * FF, lambda: lib.hd_swiglu(pt(gt), pt(up), pt(sw), S * FF)),
+        ("qkv_epilogue [16640 x 6144] -> q, k, V^T", 4 * S * (NH + 2 * NKV) * D + S * 64 * 8,
+         lambda: lib.hd_qkv_epilogue(pt(qkv), pt(qn), pt(kn), pt(cs), pt(q), pt(k), None, pt(vt), 1, S,
+                                     NH, NKV, D, 1e-6)),
+        ("apply_rotary [32 x 16640 x 128] (fp32 cos/sin tables)", 4 * NH * S * D + 8 * S * D,
+         lambda: lib.hd_apply_rotary(pt(qh), pt(cc), pt(ss), pt(qo), NH, S, D)),
+        ("head_split [16640 x 32 x 128]", 4 * E, lambda: lib.hd_head_split(pt(hs), pt(qo), S, NH, D)),
+        ("sched_vcond [16384 x 3072] bf16, bf16 -> fp32", 8 * I * P,
+         lambda: lib.hd_sched_vcond(pt(z), pt(xp), 0.5, pt(mo), I * P)),
+        ("sched_cfg_guided [16384 x 3072] fp32", 12 * I * P,
+         lambda: lib.hd_sched_cfg_guided(pt(mo), pt(mu), 5.0, pt(mg), I * P)),
+        ("sched_flow_match_step [16384 x 3072] bf16 + fp32 -> bf16", 8 * I * P,
+         lambda: lib.hd_sched_flow_match_step(pt(z), pt(mo), 0.5, 0.45, pt(zn), I * P)),
+        ("patchify_bf16 3 x 4096^2 fp32 -> [16384 x 3072] bf16", 6 * I * P,
+         lambda: lib.hd_patchify_bf16(pt(img), pt(tok), 3, 128, 128, 32)),
+    ]
+    rows = []
+    for name, nbytes, fn in cases:
+        for _ in range(3):
+            fn()
+        pkg.check_prim(name)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / iters
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        rows.append({"kernel": name, "bytes": int(nbytes), "us": round(ms * 1e3, 2),
+                     "GB_s": round(gbs, 1), "frac_of_8TBs": round(gbs / (PEAK_HBM / 1e9), 3)})
+    print(json.dumps({"elementwise": rows, "peak_GB_s": PEAK_HBM / 1e9}))
 
 
 def read_traffic():

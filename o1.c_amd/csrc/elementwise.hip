@@ -320,6 +320,8 @@ extern "C" void hd_rope_table(const float *pos_dev, int seq, const int64_t *sect
     hd_check_launch("rope_table");
 }
 
+static bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
 // Rotate-half rotation on [heads, seq, dim] (rope.cu:97-134 / :157-180).
 template <bool PEROP>
 __global__ void rotary_kernel(const uint16_t *x, const float *cosd, const float *sind, uint16_t *y,
@@ -343,11 +345,55 @@ __global__ void rotary_kernel(const uint16_t *x, const float *cosd, const float 
     }
     y[idx] = f2bf(v);
 }
+// 16-byte variant (dim % 16 == 0, aligned operands): one thread rotates 8
+// consecutive pairs (d, d + dim/2) of one row, the same arithmetic per
+// element as rotary_kernel<true> (bf16 rounding of each product).
+__global__ void rotary16_kernel(const uint16_t *x, const float *cosd, const float *sind, uint16_t *y,
+                                int heads, int seq, int dim) {
+    const int half = dim / 2, c8 = half / 8;
+    const size_t total = (size_t)heads * seq * c8;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int d0 = (int)(idx % c8) * 8;
+    const size_t hs = idx / c8;
+    const int s = hs % seq;
+    const uint16_t *xr = x + hs * dim;
+    const float *cr = cosd + (size_t)s * dim, *sr = sind + (size_t)s * dim;
+    const u32x4_t lo = *(const u32x4_t *)(xr + d0), hi = *(const u32x4_t *)(xr + half + d0);
+    const f32x4_t cl0 = *(const f32x4_t *)(cr + d0), cl1 = *(const f32x4_t *)(cr + d0 + 4);
+    const f32x4_t ch0 = *(const f32x4_t *)(cr + half + d0), ch1 = *(const f32x4_t *)(cr + half + d0 + 4);
+    const f32x4_t sl0 = *(const f32x4_t *)(sr + d0), sl1 = *(const f32x4_t *)(sr + d0 + 4);
+    const f32x4_t sh0 = *(const f32x4_t *)(sr + half + d0), sh1 = *(const f32x4_t *)(sr + half + d0 + 4);
+    u32x4_t olo, ohi;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        float r0[2], r1[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int k = 2 * e + t;
+            const float a = t ? hi_bf(lo[e]) : lo_bf(lo[e]);   // x[d]
+            const float b = t ? hi_bf(hi[e]) : lo_bf(hi[e]);   // x[d + half]
+            const float cl = k < 4 ? cl0[k] : cl1[k - 4], ch = k < 4 ? ch0[k] : ch1[k - 4];
+            const float sl = k < 4 ? sl0[k] : sl1[k - 4], sh = k < 4 ? sh0[k] : sh1[k - 4];
+            r0[t] = bfround(a * cl) - bfround(b * sl);
+            r1[t] = bfround(b * ch) + bfround(a * sh);
+        }
+        olo[e] = pack_bf2(r0[0], r0[1]);
+        ohi[e] = pack_bf2(r1[0], r1[1]);
+    }
+    *(u32x4_t *)(y + hs * dim + d0) = olo;
+    *(u32x4_t *)(y + hs * dim + half + d0) = ohi;
+}
 extern "C" void hd_apply_rotary(const void *x, const float *c, const float *s, void *y, int heads,
                                 int seq, int dim) {
     if (!x || !c || !s || !y || heads <= 0 || seq <= 0 || dim <= 0) BAD("apply_rotary");
-    rotary_kernel<true><<<hd_cdiv((size_t)heads * seq * dim, 256), 256, 0, hd_stream()>>>(
-        (const uint16_t *)x, c, s, (uint16_t *)y, heads, seq, dim);
+    if (dim % 16 == 0 && al16(x) && al16(c) && al16(s) && al16(y)) {
+        rotary16_kernel<<<hd_cdiv((size_t)heads * seq * (dim / 16), 256), 256, 0, hd_stream()>>>(
+            (const uint16_t *)x, c, s, (uint16_t *)y, heads, seq, dim);
+    } else {
+        rotary_kernel<true><<<hd_cdiv((size_t)heads * seq * dim, 256), 256, 0, hd_stream()>>>(
+            (const uint16_t *)x, c, s, (uint16_t *)y, heads, seq, dim);
+    }
     hd_check_launch("apply_rotary");
 }
 extern "C" void hd_apply_rotary_f32(const void *x, const float *c, const float *s, void *y,
@@ -377,7 +423,14 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const int ncol = (heads + 2 * kv_heads) * D;
     const uint16_t *src = qkv + (size_t)m * ncol + (size_t)hslot * D;
     float x0 = bf2f(src[lane]), x1 = bf2f(src[lane + 64]);
-    float ss = wave_sum(fmaf(x0, x0, x1 * x1));
+    // the q/k norm's summation tree: partners 4, 2, 1, then 32, 16, 8 apart
+    float ss = fmaf(x0, x0, x1 * x1);
+    ss += __shfl_xor(ss, 4, 64);
+    ss += __shfl_xor(ss, 2, 64);
+    ss += __shfl_xor(ss, 1, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 8, 64);
     float inv = 1.0f / sqrtf(ss / (float)D + eps);
     const uint16_t *w = hslot < heads ? qn_w : kn_w;
     float y0 = bfround(bf2f(w[lane]) * x0 * inv);
@@ -428,6 +481,112 @@ __global__ __launch_bounds__(256) void v_layout_kernel(const uint16_t *__restric
     }
 }
 
+// 16-byte variant of qk_norm_rope_kernel: 8 lanes per (row, head); lane j
+// holds elements 8j..8j+7 and their rotate-half partners 64+8j..64+8j+7
+// (two 16-byte loads), so x_l^2 + x_{l+64}^2 and the rotation stay inside the
+// lane. The sum of squares follows the same tree as qk_norm_rope_kernel
+// (pairs 4, 2, 1 apart inside the lane, then 32, 16, 8 apart = lanes 4, 2,
+// 1 apart), so results are bit-identical. For 16-byte aligned operands.
+__global__ __launch_bounds__(256) void qk_norm_rope16_kernel(
+    const uint16_t *__restrict__ qkv, const uint16_t *__restrict__ qn_w,
+    const uint16_t *__restrict__ kn_w, const float2 *__restrict__ cs,
+    uint16_t *__restrict__ q, uint16_t *__restrict__ k, int rows, int seq, int heads,
+    int kv_heads, float eps) {
+    const int D = 128;
+    const int j = threadIdx.x & 7;
+    const int nh = heads + kv_heads;
+    const size_t hr = (size_t)blockIdx.x * 32 + (threadIdx.x >> 3);   // (row, head slot)
+    const bool live = hr < (size_t)rows * nh;
+    const int m = live ? (int)(hr / nh) : 0, hslot = live ? (int)(hr % nh) : 0;
+    const int ncol = (heads + 2 * kv_heads) * D;
+    const int d0 = j * 8;
+    const uint16_t *src = qkv + (size_t)m * ncol + (size_t)hslot * D;
+    u32x4_t xa = {0u, 0u, 0u, 0u}, xb = {0u, 0u, 0u, 0u};
+    if (live) {
+        xa = *(const u32x4_t *)(src + d0);
+        xb = *(const u32x4_t *)(src + 64 + d0);
+    }
+    float a[8], b[8];   // x_l, x_{l+64}
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        a[2 * e] = lo_bf(xa[e]); a[2 * e + 1] = hi_bf(xa[e]);
+        b[2 * e] = lo_bf(xb[e]); b[2 * e + 1] = hi_bf(xb[e]);
+    }
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = fmaf(a[e], a[e], b[e] * b[e]);
+    // pairs 4 apart, then 2, then 1 (inside the lane)
+    const float s0 = v[0] + v[4], s1 = v[1] + v[5], s2 = v[2] + v[6], s3 = v[3] + v[7];
+    float ss = (s0 + s2) + (s1 + s3);
+    ss += __shfl_xor(ss, 4, 64);
+    ss += __shfl_xor(ss, 2, 64);
+    ss += __shfl_xor(ss, 1, 64);
+    const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+    const uint16_t *w = hslot < heads ? qn_w : kn_w;
+    const u32x4_t wa = *(const u32x4_t *)(w + d0), wb = *(const u32x4_t *)(w + 64 + d0);
+    const int bi = m / seq, s = m % seq;
+    const float2 *cr = cs + (size_t)s * (D / 2) + d0;
+    float o0[8], o1[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float w0 = (e & 1) ? hi_bf(wa[e / 2]) : lo_bf(wa[e / 2]);
+        const float w1 = (e & 1) ? hi_bf(wb[e / 2]) : lo_bf(wb[e / 2]);
+        const float y0 = bfround(w0 * a[e] * inv), y1 = bfround(w1 * b[e] * inv);
+        const float2 r = cr[e];
+        o0[e] = bfround(y0 * r.x) - bfround(y1 * r.y);
+        o1[e] = bfround(y1 * r.x) + bfround(y0 * r.y);
+    }
+    if (!live) return;
+    uint16_t *dst;
+    if (hslot < heads) dst = q + (((size_t)bi * heads + hslot) * seq + s) * D;
+    else dst = k + (((size_t)bi * kv_heads + (hslot - heads)) * seq + s) * D;
+    *(u32x4_t *)(dst + d0) = {pack_bf2(o0[0], o0[1]), pack_bf2(o0[2], o0[3]), pack_bf2(o0[4], o0[5]),
+                              pack_bf2(o0[6], o0[7])};
+    *(u32x4_t *)(dst + 64 + d0) = {pack_bf2(o1[0], o1[1]), pack_bf2(o1[2], o1[3]), pack_bf2(o1[4], o1[5]),
+                                   pack_bf2(o1[6], o1[7])};
+}
+
+// 16-byte variant of v_layout_kernel (16-byte aligned operands): 16-byte
+// reads of the V columns and 16-byte writes of 8 consecutive V^T columns.
+__global__ __launch_bounds__(256) void v_layout16_kernel(const uint16_t *__restrict__ qkv,
+                                                         uint16_t *__restrict__ v,
+                                                         uint16_t *__restrict__ vt, int seq,
+                                                         int heads, int kv_heads) {
+    const int D = 128;
+    __shared__ uint32_t tile[64][D / 2 + 1];   // bf16 pairs, one pad word per token row
+    const int s0 = blockIdx.x * 64;
+    const int hk = blockIdx.y % kv_heads, b = blockIdx.y / kv_heads;
+    const int ncol = (heads + 2 * kv_heads) * D;
+    const int col0 = (heads + kv_heads + hk) * D;
+    const int s_pad = (seq + 63) / 64 * 64;
+    for (int i = threadIdx.x; i < 64 * D / 8; i += 256) {
+        const int t = i / (D / 8), d8 = (i % (D / 8)) * 8;
+        const int s = s0 + t;
+        u32x4_t val = {0u, 0u, 0u, 0u};
+        if (s < seq) val = *(const u32x4_t *)(qkv + ((size_t)b * seq + s) * ncol + col0 + d8);
+        if (vt) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) tile[t][d8 / 2 + e] = val[e];
+        } else if (s < seq) {
+            *(u32x4_t *)(v + (((size_t)b * kv_heads + hk) * seq + s) * D + d8) = val;
+        }
+    }
+    if (!vt) return;
+    __syncthreads();
+    uint16_t *dst = vt + ((size_t)b * kv_heads + hk) * D * (size_t)s_pad + s0;
+    for (int i = threadIdx.x; i < D * 8; i += 256) {
+        const int d = i / 8, p0 = (i % 8) * 8;
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const uint32_t a = tile[perm16_ew(p0 + 2 * e)][d / 2], c = tile[perm16_ew(p0 + 2 * e + 1)][d / 2];
+            const uint32_t lo = (d & 1) ? a >> 16 : a & 0xFFFFu, hi = (d & 1) ? c >> 16 : c & 0xFFFFu;
+            w[e] = lo | (hi << 16);
+        }
+        *(u32x4_t *)(dst + (size_t)d * s_pad + p0) = {w[0], w[1], w[2], w[3]};
+    }
+}
+
 extern "C" void hd_qkv_epilogue(const void *qkv_dev, const void *qn_w, const void *kn_w,
                                 const float *cs_dev, void *q_dev, void *k_dev, void *v_dev,
                                 void *vt_dev, int batch, int seq, int heads, int kv_heads,
@@ -435,14 +594,26 @@ extern "C" void hd_qkv_epilogue(const void *qkv_dev, const void *qn_w, const voi
     if (!qkv_dev || !qn_w || !kn_w || !cs_dev || !q_dev || !k_dev || (!v_dev && !vt_dev) ||
         batch <= 0 || seq <= 0 || heads <= 0 || kv_heads <= 0 || head_dim != 128)
         BAD("qkv_epilogue");
-    dim3 g1(batch * seq, hd_cdiv(heads + kv_heads, 4));
-    qk_norm_rope_kernel<<<g1, 256, 0, hd_stream()>>>(
-        (const uint16_t *)qkv_dev, (const uint16_t *)qn_w, (const uint16_t *)kn_w,
-        (const float2 *)cs_dev, (uint16_t *)q_dev, (uint16_t *)k_dev, seq, heads, kv_heads, eps);
+    if (al16(qkv_dev) && al16(qn_w) && al16(kn_w) && al16(cs_dev) && al16(q_dev) && al16(k_dev)) {
+        const size_t nhr = (size_t)batch * seq * (heads + kv_heads);
+        qk_norm_rope16_kernel<<<hd_cdiv(nhr, 32), 256, 0, hd_stream()>>>(
+            (const uint16_t *)qkv_dev, (const uint16_t *)qn_w, (const uint16_t *)kn_w,
+            (const float2 *)cs_dev, (uint16_t *)q_dev, (uint16_t *)k_dev, batch * seq, seq, heads,
+            kv_heads, eps);
+    } else {
+        dim3 g1(batch * seq, hd_cdiv(heads + kv_heads, 4));
+        qk_norm_rope_kernel<<<g1, 256, 0, hd_stream()>>>(
+            (const uint16_t *)qkv_dev, (const uint16_t *)qn_w, (const uint16_t *)kn_w,
+            (const float2 *)cs_dev, (uint16_t *)q_dev, (uint16_t *)k_dev, seq, heads, kv_heads, eps);
+    }
     hd_check_launch("qkv_epilogue(qk)");
     dim3 g2(hd_cdiv(seq, 64), batch * kv_heads);
-    v_layout_kernel<<<g2, 256, 0, hd_stream()>>>((const uint16_t *)qkv_dev, (uint16_t *)v_dev,
-                                                 (uint16_t *)vt_dev, seq, heads, kv_heads);
+    if (al16(qkv_dev) && (vt_dev ? al16(vt_dev) && ((seq + 63) / 64 * 64) % 8 == 0 : al16(v_dev)))
+        v_layout16_kernel<<<g2, 256, 0, hd_stream()>>>((const uint16_t *)qkv_dev, (uint16_t *)v_dev,
+                                                       (uint16_t *)vt_dev, seq, heads, kv_heads);
+    else
+        v_layout_kernel<<<g2, 256, 0, hd_stream()>>>((const uint16_t *)qkv_dev, (uint16_t *)v_dev,
+                                                     (uint16_t *)vt_dev, seq, heads, kv_heads);
     hd_check_launch("qkv_epilogue(v)");
 }
 
@@ -491,16 +662,41 @@ __global__ void head_perm_kernel(const uint16_t *in, uint16_t *out, int seq, int
         out[idx] = in[((size_t)h * seq + s) * d + dd];
     }
 }
+// 16-byte variant (dim % 8 == 0, 16-byte aligned operands): one thread
+// moves 8 consecutive elements of a row; the same permutation.
+template <bool SPLIT>
+__global__ void head_perm16_kernel(const u32x4_t *in, u32x4_t *out, int seq, int heads, int d8) {
+    const size_t total = (size_t)seq * heads * d8;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int dd = idx % d8;
+    const size_t r = idx / d8;
+    if (SPLIT) {
+        const int s = r % seq, h = r / seq;
+        out[idx] = in[((size_t)s * heads + h) * d8 + dd];
+    } else {
+        const int h = r % heads, s = r / heads;
+        out[idx] = in[((size_t)h * seq + s) * d8 + dd];
+    }
+}
+template <bool SPLIT>
+static void launch_head_perm(const void *in, void *out, int seq, int heads, int dim) {
+    if (dim % 8 == 0 && al16(in) && al16(out)) {
+        head_perm16_kernel<SPLIT><<<hd_cdiv((size_t)seq * heads * (dim / 8), 256), 256, 0, hd_stream()>>>(
+            (const u32x4_t *)in, (u32x4_t *)out, seq, heads, dim / 8);
+    } else {
+        head_perm_kernel<SPLIT><<<hd_cdiv((size_t)seq * heads * dim, 256), 256, 0, hd_stream()>>>(
+            (const uint16_t *)in, (uint16_t *)out, seq, heads, dim);
+    }
+}
 extern "C" void hd_head_split(const void *in, void *out, int seq, int heads, int dim) {
     if (!in || !out || seq <= 0 || heads <= 0 || dim <= 0) BAD("head_split");
-    head_perm_kernel<true><<<hd_cdiv((size_t)seq * heads * dim, 256), 256, 0, hd_stream()>>>(
-        (const uint16_t *)in, (uint16_t *)out, seq, heads, dim);
+    launch_head_perm<true>(in, out, seq, heads, dim);
     hd_check_launch("head_split");
 }
 extern "C" void hd_head_merge(const void *in, void *out, int seq, int heads, int dim) {
     if (!in || !out || seq <= 0 || heads <= 0 || dim <= 0) BAD("head_merge");
-    head_perm_kernel<false><<<hd_cdiv((size_t)seq * heads * dim, 256), 256, 0, hd_stream()>>>(
-        (const uint16_t *)in, (uint16_t *)out, seq, heads, dim);
+    launch_head_perm<false>(in, out, seq, heads, dim);
     hd_check_launch("head_merge");
 }
 
@@ -600,38 +796,130 @@ __global__ void cfg_kernel(const float *c, const float *u, float g, float *o, in
     int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) o[i] = fmaf(g, c[i], (1.0f - g) * u[i]);
 }
+// 4-wide variants of the sampler kernels: one thread per 4 consecutive
+// elements (16-byte fp32 / 8-byte bf16 accesses), the same per-element
+// arithmetic as the scalar kernels above (each functor's `one` is that
+// arithmetic; `vec` applies it to 4 loaded elements). The last thread does
+// its partial group element by element. Taken when every operand is 16-byte
+// aligned; otherwise the scalar kernels run.
+__device__ __forceinline__ void ld4b(const uint16_t *p, size_t i, float v[4]) {
+    const u32x2_t w = *(const u32x2_t *)(p + i);
+    v[0] = lo_bf(w[0]); v[1] = hi_bf(w[0]); v[2] = lo_bf(w[1]); v[3] = hi_bf(w[1]);
+}
+struct PwUpcast {
+    const uint16_t *in; float *out;
+    __device__ void one(size_t i) const { out[i] = bf2f(in[i]); }
+    __device__ void vec(size_t i) const {
+        float v[4];
+        ld4b(in, i, v);
+        *(f32x4_t *)(out + i) = {v[0], v[1], v[2], v[3]};
+    }
+};
+struct PwDenoised {
+    const float *z, *mo; float sigma; float *o;
+    __device__ float f(float zv, float m) const { return fmaf(-m, sigma, zv); }
+    __device__ void one(size_t i) const { o[i] = f(z[i], mo[i]); }
+    __device__ void vec(size_t i) const {
+        const f32x4_t a = *(const f32x4_t *)(z + i), b = *(const f32x4_t *)(mo + i);
+        *(f32x4_t *)(o + i) = {f(a[0], b[0]), f(a[1], b[1]), f(a[2], b[2]), f(a[3], b[3])};
+    }
+};
+struct PwZnext {
+    const float *noise, *den; float sn, s_noise; float *o;
+    __device__ float f(float nz, float d) const { return fmaf(1.0f - sn, d, (sn * nz) * s_noise); }
+    __device__ void one(size_t i) const { o[i] = f(noise[i], den[i]); }
+    __device__ void vec(size_t i) const {
+        const f32x4_t a = *(const f32x4_t *)(noise + i), b = *(const f32x4_t *)(den + i);
+        *(f32x4_t *)(o + i) = {f(a[0], b[0]), f(a[1], b[1]), f(a[2], b[2]), f(a[3], b[3])};
+    }
+};
+struct PwVcond {
+    const uint16_t *z, *xp; float sigma; float *mo;
+    __device__ void one(size_t i) const { mo[i] = (bf2f(z[i]) - bf2f(xp[i])) / sigma; }
+    __device__ void vec(size_t i) const {
+        float a[4], b[4];
+        ld4b(z, i, a);
+        ld4b(xp, i, b);
+        *(f32x4_t *)(mo + i) = {(a[0] - b[0]) / sigma, (a[1] - b[1]) / sigma, (a[2] - b[2]) / sigma,
+                                (a[3] - b[3]) / sigma};
+    }
+};
+struct PwFmStep {
+    const uint16_t *z; const float *mo; float dt; uint16_t *zn;
+    __device__ void one(size_t i) const { zn[i] = f2bf(fmaf(dt, mo[i], bf2f(z[i]))); }
+    __device__ void vec(size_t i) const {
+        float a[4];
+        ld4b(z, i, a);
+        const f32x4_t m = *(const f32x4_t *)(mo + i);
+        *(u32x2_t *)(zn + i) = {pack_bf2(fmaf(dt, m[0], a[0]), fmaf(dt, m[1], a[1])),
+                                pack_bf2(fmaf(dt, m[2], a[2]), fmaf(dt, m[3], a[3]))};
+    }
+};
+struct PwCfg {
+    const float *c, *u; float g; float *o;
+    __device__ float f(float cv, float uv) const { return fmaf(g, cv, (1.0f - g) * uv); }
+    __device__ void one(size_t i) const { o[i] = f(c[i], u[i]); }
+    __device__ void vec(size_t i) const {
+        const f32x4_t a = *(const f32x4_t *)(c + i), b = *(const f32x4_t *)(u + i);
+        *(f32x4_t *)(o + i) = {f(a[0], b[0]), f(a[1], b[1]), f(a[2], b[2]), f(a[3], b[3])};
+    }
+};
+template <class F>
+__global__ void pw4_kernel(F f, int n) {
+    const size_t i0 = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i0 + 4 <= (size_t)n) {
+        f.vec(i0);
+    } else {
+        for (size_t i = i0; i < (size_t)n; i++) f.one(i);
+    }
+}
+template <class F>
+static void launch_pw4(const F &f, int n) {
+    pw4_kernel<F><<<hd_cdiv(hd_cdiv(n, 4), 256), 256, 0, hd_stream()>>>(f, n);
+}
+
 extern "C" void hd_sched_bf16_upcast(const void *in, float *out, int n) {
     if (!in || !out || n <= 0) BAD("sched_bf16_upcast");
-    upcast_kernel<<<hd_cdiv(n, 256), 256, 0, hd_stream()>>>((const uint16_t *)in, out, n);
+    if (al16(in) && al16(out)) launch_pw4(PwUpcast{(const uint16_t *)in, out}, n);
+    else upcast_kernel<<<hd_cdiv(n, 256), 256, 0, hd_stream()>>>((const uint16_t *)in, out, n);
     hd_check_launch("sched_bf16_upcast");
 }
 extern "C" void hd_sched_denoised(const float *z, const float *mo, float sigma, float *o, int n) {
     if (!z || !mo || !o || n <= 0) BAD("sched_denoised");
-    denoised_kernel<<<hd_cdiv(n, 256), 256, 0, hd_stream()>>>(z, mo, sigma, o, n);
+    if (al16(z) && al16(mo) && al16(o)) launch_pw4(PwDenoised{z, mo, sigma, o}, n);
+    else denoised_kernel<<<hd_cdiv(n, 256), 256, 0, hd_stream()>>>(z, mo, sigma, o, n);
     hd_check_launch("sched_denoised");
 }
 extern "C" void hd_sched_z_next(const float *noise, const float *den, float sn, float s_noise,
                                 float *o, int n) {
     if (!noise || !den || !o || n <= 0) BAD("sched_z_next");
-    znext_kernel<<<hd_cdiv(n, 256), 256, 0, hd_stream()>>>(noise, den, sn, s_noise, o, n);
+    if (al16(noise) && al16(den) && al16(o)) launch_pw4(PwZnext{noise, den, sn, s_noise, o}, n);
+    else znext_kernel<<<hd_cdiv(n, 256), 256, 0, hd_stream()>>>(noise, den, sn, s_noise, o, n);
     hd_check_launch("sched_z_next");
 }
 extern "C" void hd_sched_vcond(const void *z, const void *xp, float sigma, float *mo, int n) {
     if (!z || !xp || !mo || n <= 0) BAD("sched_vcond");
-    vcond_kernel<<<hd_cdiv(n, 256), 256, 0, hd_stream()>>>((const uint16_t *)z, (const uint16_t *)xp,
-                                                           sigma, mo, n);
+    if (al16(z) && al16(xp) && al16(mo))
+        launch_pw4(PwVcond{(const uint16_t *)z, (const uint16_t *)xp, sigma, mo}, n);
+    else
+        vcond_kernel<<<hd_cdiv(n, 256), 256, 0, hd_stream()>>>((const uint16_t *)z, (const uint16_t *)xp,
+                                                               sigma, mo, n);
     hd_check_launch("sched_vcond");
 }
 extern "C" void hd_sched_flow_match_step(const void *z, const float *mo, float sigma,
                                          float sigma_next, void *zn, int n) {
     if (!z || !mo || !zn || n <= 0) BAD("sched_flow_match_step");
-    fm_step_kernel<<<hd_cdiv(n, 256), 256, 0, hd_stream()>>>((const uint16_t *)z, mo,
-                                                             sigma_next - sigma, (uint16_t *)zn, n);
+    if (al16(z) && al16(mo) && al16(zn))
+        launch_pw4(PwFmStep{(const uint16_t *)z, mo, sigma_next - sigma, (uint16_t *)zn}, n);
+    else
+        fm_step_kernel<<<hd_cdiv(n, 256), 256, 0, hd_stream()>>>((const uint16_t *)z, mo,
+                                                                 sigma_next - sigma, (uint16_t *)zn, n);
     hd_check_launch("sched_flow_match_step");
 }
 extern "C" void hd_sched_cfg_guided(const float *c, const float *u, float g, float *o, int n) {
     if (!c || !u || !o || n <= 0) BAD("sched_cfg_guided");
-    cfg_kernel<<<hd_cdiv(n, 256), 256, 0, hd_stream()>>>(c, u, g, o, n);
+    if (al16(c) && al16(u) && al16(o)) launch_pw4(PwCfg{c, u, g, o}, n);
+    else cfg_kernel<<<hd_cdiv(n, 256), 256, 0, hd_stream()>>>(c, u, g, o, n);
     hd_check_launch("sched_cfg_guided");
 }
 
@@ -712,21 +1000,51 @@ __global__ void patch_kernel(const float *src, TO *dst, int C, int Hp, int Wp, i
         dst[pix] = src[idx];
     }
 }
+// 4-wide variant (p % 4 == 0, aligned operands): one thread moves 4
+// consecutive pixels of a patch row (16-byte image accesses), the same index
+// rule and conversion per element.
+template <int DIR, typename TO>
+__global__ void patch4_kernel(const float *src, TO *dst, int C, int Hp, int Wp, int p) {
+    const size_t feats = (size_t)C * p * p;
+    const size_t total = (size_t)Hp * Wp * feats / 4;
+    const size_t idx4 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx4 >= total) return;
+    const size_t idx = idx4 * 4;
+    const size_t tok = idx / feats;
+    const int f = idx % feats;
+    const int ch = f / (p * p), i = (f / p) % p, j = f % p;
+    const int r = tok / Wp, c = tok % Wp;
+    const size_t pix = ((size_t)ch * Hp * p + (size_t)(r * p + i)) * ((size_t)Wp * p) + (size_t)(c * p + j);
+    if (DIR == 0) {
+        const f32x4_t v = *(const f32x4_t *)(src + pix);
+        if constexpr (sizeof(TO) == 2)
+            *(u32x2_t *)((uint16_t *)dst + idx) = {pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+        else
+            *(f32x4_t *)((float *)dst + idx) = v;
+    } else {
+        *(f32x4_t *)((float *)dst + pix) = *(const f32x4_t *)(src + idx);
+    }
+}
+template <int DIR, typename TO>
+static void launch_patch(const float *src, TO *dst, int C, int Hp, int Wp, int p) {
+    const size_t total = (size_t)C * Hp * Wp * p * p;
+    if (p % 4 == 0 && al16(src) && al16(dst))
+        patch4_kernel<DIR, TO><<<hd_cdiv(total / 4, 256), 256, 0, hd_stream()>>>(src, dst, C, Hp, Wp, p);
+    else
+        patch_kernel<DIR, TO><<<hd_cdiv(total, 256), 256, 0, hd_stream()>>>(src, dst, C, Hp, Wp, p);
+}
 extern "C" void hd_patchify_f32(const float *img, float *tok, int C, int Hp, int Wp, int p) {
     if (!img || !tok || C <= 0 || Hp <= 0 || Wp <= 0 || p <= 0) BAD("patchify");
-    patch_kernel<0, float><<<hd_cdiv((size_t)C * Hp * Wp * p * p, 256), 256, 0, hd_stream()>>>(
-        img, tok, C, Hp, Wp, p);
+    launch_patch<0, float>(img, tok, C, Hp, Wp, p);
     hd_check_launch("patchify");
 }
 extern "C" void hd_unpatchify_f32(const float *tok, float *img, int C, int Hp, int Wp, int p) {
     if (!img || !tok || C <= 0 || Hp <= 0 || Wp <= 0 || p <= 0) BAD("unpatchify");
-    patch_kernel<1, float><<<hd_cdiv((size_t)C * Hp * Wp * p * p, 256), 256, 0, hd_stream()>>>(
-        tok, img, C, Hp, Wp, p);
+    launch_patch<1, float>(tok, img, C, Hp, Wp, p);
     hd_check_launch("unpatchify");
 }
 extern "C" void hd_patchify_bf16(const float *img, void *tok, int C, int Hp, int Wp, int p) {
     if (!img || !tok || C <= 0 || Hp <= 0 || Wp <= 0 || p <= 0) BAD("patchify_bf16");
-    patch_kernel<0, uint16_t><<<hd_cdiv((size_t)C * Hp * Wp * p * p, 256), 256, 0, hd_stream()>>>(
-        img, (uint16_t *)tok, C, Hp, Wp, p);
+    launch_patch<0, uint16_t>(img, (uint16_t *)tok, C, Hp, Wp, p);
     hd_check_launch("patchify_bf16");
 }

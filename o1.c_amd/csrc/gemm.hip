@@ -343,8 +343,8 @@ template <int CPR> __device__ __forceinline__ int ms_swz(int r) {
 // EPI_QKV epilogue for one wave: its WTM rows x 128 columns (one head) are
 // staged in LDS as the bf16 projection output (the reference's rounding
 // point). q/k heads: lane-per-row RMSNorm (the sum of squares uses the
-// pairing and butterfly order of the standalone kernel, x_l^2 + x_{l+64}^2
-// then xor 32..1, so results are bit-identical) and rotate-half rotary with
+// pairing and summation tree of the standalone kernels, x_l^2 + x_{l+64}^2
+// then pairs 4, 2, 1 and 32, 16, 8 apart, so results are bit-identical) and rotate-half rotary with
 // bf16 rounding of every product, then coalesced stores to [B,H,S,128].
 // v heads: transposed stores into [B,KV,128,S] with key bits 2 and 3
 // exchanged (the flash kernel's V^T layout; S % 64 == 0 so no padding).
@@ -371,10 +371,18 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs &g, uint16_t *stg, i
                     v[c * 8 + 2 * e + 1] = fmaf(a1, a1, b1 * b1);
                 }
             }
+            // the q/k norm's summation tree (shared by every q/k norm
+            // kernel): pairs 4, 2, 1 apart inside each group of 8, then the
+            // group sums 32, 16, 8 apart
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1)
+            for (int o = 4; o > 0; o >>= 1)
 #pragma unroll
-                for (int k = 0; k < o; k++) v[k] = v[k] + v[k + o];
+                for (int k = 0; k < 64; k++)
+                    if ((k & 7) < o) v[k] = v[k] + v[k + o];
+#pragma unroll
+            for (int o = 32; o >= 8; o >>= 1)
+#pragma unroll
+                for (int k = 0; k < o; k += 8) v[k] = v[k] + v[k + o];
             const float inv = 1.0f / sqrtf(v[0] / 128.0f + g.eps);
             const int s = m % S;
             const float2 *cs = g.cs + (size_t)s * 64;

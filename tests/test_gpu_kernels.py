@@ -522,3 +522,68 @@ def test_flash_families_identical(pkg, lib, dev, S, ar_len, dense):
         lib.hd_flash_set_family(prev)
     assert torch.equal(outs[0], outs[1])
     assert float(outs[0].float().abs().sum(dim=-1).min()) > 0
+
+
+@pytest.mark.parametrize("n,off", [(12291, 0), (12291, 1), (7, 0)])
+def test_sched_vector_paths_bit_exact(pkg, lib, dev, n, off):
+    """The sampler kernels' 4-wide path (aligned operands; a partial last
+    group when n % 4 != 0) and the scalar fallback (operands one element off
+    16-byte alignment) both equal the oracle bit for bit; so do the fp32
+    denoised / z_next / bf16 upcast pointwise steps against numpy's fp32
+    fma (sched.cu:21-72)."""
+    rng = np.random.default_rng(n + off)
+    z = orc.bf16_round(rng.standard_normal(n))
+    xp = orc.bf16_round(rng.standard_normal(n))
+    # allocate one element more and view from `off`, so off = 1 misaligns
+    zb = torch.zeros(n + 1, dtype=torch.bfloat16, device=dev)
+    xb = torch.zeros(n + 1, dtype=torch.bfloat16, device=dev)
+    zb[off:off + n] = torch.from_numpy(z.astype(np.float32)).to(torch.bfloat16)
+    xb[off:off + n] = torch.from_numpy(xp.astype(np.float32)).to(torch.bfloat16)
+    zd, xd = zb[off:off + n], xb[off:off + n]
+    mo = torch.empty(n + 1, device=dev)[off:off + n]
+    lib.hd_sched_vcond(pkg.ptr(zd), pkg.ptr(xd), 0.7, pkg.ptr(mo), n)
+    assert np.array_equal(mo.cpu().numpy(), orc.sched_vcond(z, xp, 0.7))
+    zn = torch.empty(n + 1, dtype=torch.bfloat16, device=dev)[off:off + n]
+    lib.hd_sched_flow_match_step(pkg.ptr(zd), pkg.ptr(mo), 0.7, 0.6, pkg.ptr(zn), n)
+    assert np.array_equal(host(zn), orc.sched_flow_match_step(z, mo.cpu().numpy(), 0.7, 0.6))
+    c = rng.standard_normal(n).astype(np.float32)
+    u = rng.standard_normal(n).astype(np.float32)
+    cd = torch.zeros(n + 1, device=dev)
+    ud = torch.zeros(n + 1, device=dev)
+    cd[off:off + n] = torch.from_numpy(c).to(dev)
+    ud[off:off + n] = torch.from_numpy(u).to(dev)
+    cv, uv = cd[off:off + n], ud[off:off + n]
+    o = torch.empty(n + 1, device=dev)[off:off + n]
+    lib.hd_sched_cfg_guided(pkg.ptr(cv), pkg.ptr(uv), 5.0, pkg.ptr(o), n)
+    assert np.array_equal(o.cpu().numpy(), orc.sched_cfg_guided(c, u, 5.0))
+    f32 = np.float32
+    lib.hd_sched_denoised(pkg.ptr(cv), pkg.ptr(uv), 0.3, pkg.ptr(o), n)
+    want = (-u.astype(np.float64) * f32(0.3) + c).astype(np.float32)   # one rounding: fma
+    assert np.array_equal(o.cpu().numpy(), want)
+    lib.hd_sched_z_next(pkg.ptr(cv), pkg.ptr(uv), 0.4, 1.0, pkg.ptr(o), n)
+    t = (f32(0.4) * c).astype(np.float32) * f32(1.0)
+    want = (f32(1.0) - f32(0.4)).astype(np.float64) * u + t.astype(np.float64)
+    assert np.array_equal(o.cpu().numpy(), want.astype(np.float32))
+    lib.hd_sched_bf16_upcast(pkg.ptr(zd), pkg.ptr(o), n)
+    assert np.array_equal(o.cpu().numpy(), z.astype(np.float32))
+
+
+def test_patchify_bf16_and_rotary_scalar_path(pkg, lib, dev):
+    """patchify_bf16 (4-wide path) equals the oracle's patchify rounded to
+    bf16; a head_dim of 24 (not a multiple of 16) takes the scalar rotary
+    kernel, which must equal the oracle bit for bit as the 16-byte one does."""
+    rng = np.random.default_rng(5)
+    img = rng.standard_normal((3, 64, 96)).astype(np.float32)
+    tok = torch.empty(2 * 3, 3 * 32 * 32, dtype=torch.bfloat16, device=dev)
+    imgd = torch.from_numpy(img).to(dev)
+    lib.hd_patchify_bf16(pkg.ptr(imgd), pkg.ptr(tok), 3, 2, 3, 32)
+    assert np.array_equal(host(tok), orc.bf16_round(orc.patchify(img, 32)))
+    seq, dim = 5, 24
+    x = orc.bf16_round(rng.standard_normal((2, seq, dim)))
+    cr = rng.standard_normal((seq, dim)).astype(np.float32)
+    sr = rng.standard_normal((seq, dim)).astype(np.float32)
+    y = torch.empty(2, seq, dim, dtype=torch.bfloat16, device=dev)
+    xd, cd, sd = dbf(x, dev), torch.from_numpy(cr).to(dev), torch.from_numpy(sr).to(dev)
+    lib.hd_apply_rotary(pkg.ptr(xd), pkg.ptr(cd), pkg.ptr(sd), pkg.ptr(y), 2, seq, dim)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(y), orc.apply_rotary(x, cr, sr, 1))
