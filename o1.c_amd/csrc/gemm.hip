@@ -542,7 +542,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
     const int nb_a = (int)((size_t)g.M * g.K * 2), nb_b = (int)((size_t)brows * g.K * 2);
     uint32_t a_vo[AI], b_vo[BI];
     int b_rs[BI];
-    if constexpr (LDR == 5) {
+    if constexpr (LDR == 5 || LDR == 6) {
 #pragma unroll
         for (int i = 0; i < AI; i++) {
             const int r = (wave * AI + i) * C::RPI + sub;
@@ -569,7 +569,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
     auto issue = [&](int kt, int st) {
         if (LDR == 3) return;   // diagnostic: no global->LDS traffic
         uint16_t *As = smem + st * C::STAGE, *Bs = As + BM * BK;
-        if constexpr (LDR == 5) {
+        if constexpr (LDR == 5 || LDR == 6) {
             const uint32_t so = (uint32_t)(kbase + kt) * BK * 2;
 #pragma unroll
             for (int i = 0; i < AI; i++)
@@ -795,6 +795,10 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
                     }
             return;
         }
+    }
+    if constexpr (LDR == 6) {   // diagnostic (timing only): no epilogue
+        if (acc[0][0][0] == 12345.f) g.C[threadIdx.x] = 1;   // keeps the K loop live
+        return;
     }
     __syncthreads();   // every wave is done with the ring before staging reuses it
 
@@ -1325,6 +1329,7 @@ static bool run_table(int cfg, GemmArgs &g) {
     case 44: launch_ms<256, 256, 32, 3, 2, 2, EPI, 3, 1, 5>(g); return true;
     case 50: launch_ms<256, 256, 64, 2, 2, 4, EPI, 3, 1, 5>(g); return true;  // 8-wave ring, buffer loads
     case 51: launch_ms<192, 256, 64, 2, 2, 4, EPI, 3, 1, 5>(g); return true;
+    case 55: launch_ms<256, 256, 64, 2, 2, 4, EPI, 3, 1, 6>(g); return true;  // diag: no epilogue
     case 7: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 1>(g); return true;    // diag: compute only
     case 8: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 2>(g); return true;    // diag: loads only
     default: return false;
