@@ -238,6 +238,14 @@ SIGNATURES = {
     "hd_gemm_tune_run": (c_int, [c_int, c_int, P, P, P, P, c_int, c_int, c_int]),
     "hd_gemm_set_family": (c_int, [c_int]),
     "hd_flash_set_family": (c_int, [c_int]),
+    "hd_tokenizer_load": (c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p]),
+    "hd_tokenizer_unload": (None, []),
+    "hd_tokenizer_encode": (c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.POINTER(c_int)), ctypes.POINTER(c_size_t)]),
+    "hd_tokenizer_encode_prompt": (c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.POINTER(c_int)), ctypes.POINTER(c_size_t)]),
+    "hd_tokenizer_build_template": (c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]),
+    "hd_tokenizer_build_ref_template": (c_int, [ctypes.c_char_p, c_int, ctypes.POINTER(ctypes.c_void_p)]),
+    "hd_tokenizer_special_id": (c_int, [ctypes.c_char_p]),
+    "hd_tokenizer_free_ids": (None, [ctypes.POINTER(c_int)]),
     "hd_linear_qkv_rope": (c_int, [P, P, P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float]),
     "hd_linear_qkv_rope_ws": (c_int, [P] * 10 + [c_int] * 5 + [c_float, P, ctypes.c_int64]),
     # hd_sdpa.h
