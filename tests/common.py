@@ -3,6 +3,8 @@ fp32 on the host), position tables, metrics."""
 import numpy as np
 import torch
 
+VOCAB, TMS = 151936, 151673   # forward.c:274 table rows; the timestep token id
+
 BLOCK_KEYS = ("q_proj", "k_proj", "v_proj", "o_proj", "input_ln", "post_ln", "gate_proj",
               "up_proj", "down_proj", "q_norm", "k_norm")
 
@@ -144,3 +146,20 @@ class Stepper:
             self.slots = [slots[2], slots[0], slots[1]]
             self.this_order, self.lower, self.have = pl.next_this_order, pl.next_lower_order, 1
         pkg.check_prim("step %d" % i)
+
+
+def make_forward_weights(n_layers, HID, H, KV, FF, D, seed, vocab=None):
+    """Global weights of the denoiser (token table of `vocab` rows, t-embedder,
+    x_embedder, final norm and head) plus `n_layers` block weight sets."""
+    g = torch.Generator().manual_seed(seed)
+
+    def r(*shape, std=0.02):
+        return bf16(torch.randn(*shape, generator=g) * std)
+    fw = {
+        "embed_tokens": r(vocab or VOCAB, HID, std=1.0),
+        "te0_w": r(HID, 256), "te0_b": r(HID), "te2_w": r(HID, HID), "te2_b": r(HID),
+        "xe1_w": r(1024, 3072), "xe2_w": r(HID, 1024, std=0.05), "xe2_b": r(HID),
+        "fl_w": r(3072, HID), "fl_b": r(3072), "fnorm_w": bf16(1 + torch.randn(HID, generator=g) * 0.02),
+        "blocks": [make_block_weights(HID, H, KV, FF, D, seed=seed + 1 + i) for i in range(n_layers)],
+    }
+    return fw

@@ -8,26 +8,10 @@ import pytest
 import torch
 
 from oracle import oracle as orc
-from tests.common import make_block_weights, rel_l2, cosine, grid_pos, bf16, Stepper
+from tests.common import (make_block_weights, make_forward_weights, rel_l2, cosine, grid_pos, bf16,
+                          Stepper, VOCAB, TMS)
 
 pytestmark = pytest.mark.gpu
-
-VOCAB, TMS = 151936, 151673
-
-
-def make_forward_weights(n_layers, HID, H, KV, FF, D, seed):
-    g = torch.Generator().manual_seed(seed)
-
-    def r(*shape, std=0.02):
-        return bf16(torch.randn(*shape, generator=g) * std)
-    fw = {
-        "embed_tokens": r(VOCAB, HID, std=1.0),
-        "te0_w": r(HID, 256), "te0_b": r(HID), "te2_w": r(HID, HID), "te2_b": r(HID),
-        "xe1_w": r(1024, 3072), "xe2_w": r(HID, 1024, std=0.05), "xe2_b": r(HID),
-        "fl_w": r(3072, HID), "fl_b": r(3072), "fnorm_w": bf16(1 + torch.randn(HID, generator=g) * 0.02),
-        "blocks": [make_block_weights(HID, H, KV, FF, D, seed=seed + 1 + i) for i in range(n_layers)],
-    }
-    return fw
 
 
 def store_names(fw):
