@@ -165,8 +165,10 @@ hd_status hd_denoise_euler_cfg(const hd_forward_binding *bw, hd_forward_workspac
  *   HD_SAMPLER_UNIPC  default: FlowUniPC order 2 (hd_scheduler_unipc_plan +
  *                     hd_unipc_*), z = bf16(predictor output)
  * batch 2 runs classifier-free guidance (row 0 cond, row 1 uncond, combined
- * with `guidance`); batch 1 runs the conditional forward only. The sigma
- * schedule comes from `sched` (steps + 1 values). Scratch:
+ * with `guidance`) over two sequences of equal length sharing text_len and
+ * positions (pad the unconditional prompt, or use hd_denoise_cfg for the
+ * reference's shorter unconditional sequence); batch 1 runs the conditional
+ * forward only. The sigma schedule comes from `sched` (steps + 1 values). Scratch:
  * hd_denoise_run_scratch_bytes(). The flash sampler's noise is drawn on the
  * host into pinned staging while the previous step's forward runs. */
 enum { HD_SAMPLER_EULER = 0, HD_SAMPLER_FLASH = 1, HD_SAMPLER_UNIPC = 2 };
@@ -178,6 +180,28 @@ hd_status hd_denoise(const hd_forward_binding *bw, hd_forward_workspace *ws, int
                      float noise_clip_std, int seq, int heads, int kv_heads, int hidden,
                      int ff_hidden, int head_dim, int tms_token_id, void *scratch,
                      int64_t scratch_bytes, void *stream);
+
+/* hd_denoise_cfg (extension): guided generation with the unconditional
+ * branch as a sequence of its own, as the reference runs it: its " "
+ * caption gives it a shorter text (T_uncond), its own positions, causal
+ * prefix and workspace (generate.c:1075, :1119-1120, :1341). Each step runs
+ * the conditional forward over [text | image] (S = T + I rows) and the
+ * unconditional one over [text_uncond | image] (S_uncond rows) on the same
+ * latent z, combines the two velocities with `guidance` and applies the
+ * sampler, as hd_denoise with batch 2 does for equal-length sequences.
+ * ws_uncond must be a different workspace, sized for S_uncond
+ * (hd_forward_batched_workspace_bytes with batch 1). Scratch:
+ * hd_denoise_cfg_scratch_bytes(). */
+int64_t hd_denoise_cfg_scratch_bytes(int seq, int seq_uncond, int img_tokens, int steps);
+hd_status hd_denoise_cfg(const hd_forward_binding *bw, hd_forward_workspace *ws,
+                         hd_forward_workspace *ws_uncond, int sampler, const hd_scheduler *sched,
+                         int steps, const int64_t *ids_dev, int text_len, const float *pos_dev,
+                         int ar_len, int seq, const int64_t *ids_uncond_dev, int text_len_uncond,
+                         const float *pos_uncond_dev, int ar_len_uncond, int seq_uncond, void *z_dev,
+                         int img_tokens, float guidance, uint64_t seed, float s_noise_start,
+                         float s_noise_end, float noise_clip_std, int heads, int kv_heads,
+                         int hidden, int ff_hidden, int head_dim, int tms_token_id, void *scratch,
+                         int64_t scratch_bytes, void *stream);
 
 /* hd_denoise_visual: the edit / personalize loop (generate.c:855-935), batch
  * 1 with vision conditioning. Each step runs hd_forward over

@@ -589,7 +589,17 @@ struct PinnedNoise {
 };
 }  // namespace
 
-// Shared loop of hd_denoise / hd_denoise_visual. I_t target rows are
+// The unconditional branch of a guided loop when it is its own sequence
+// (generate.c:1075, :1119-1120, :1341: the " " caption gives it a shorter
+// text and its own positions, mask and workspace).
+struct UncondSeq {
+    hd_forward_workspace *ws;
+    const int64_t *ids;
+    int T, ar_len, S;
+    const float *pos;
+};
+
+// Shared loop of hd_denoise / hd_denoise_cfg / hd_denoise_visual. I_t target rows are
 // denoised; with n_ref reference rows the forward sees I_t + n_ref image
 // tokens (target first), the references either as patches copied once after
 // the target rows (`ref`) or as cached x_embedder rows (ws->xe_ref).
@@ -599,20 +609,24 @@ static hd_status denoise_loop(const hd_forward_binding *bw, hd_forward_workspace
                               const hd_visual_cond *vis, void *z, int I_t, const void *ref,
                               int n_ref, float guidance, uint64_t seed, float sn_start,
                               float sn_end, float clip, int S, int H, int KV, int HID, int FF,
-                              int D, int tms, void *scratch, int64_t scratch_bytes, void *stream) {
+                              int D, int tms, void *scratch, int64_t scratch_bytes, void *stream,
+                              const UncondSeq *u = nullptr) {
     const int I = I_t + n_ref;
     if (steps > sched->num_steps - 1) {
         hd_set_error("denoise: %d steps but the schedule has %d sigmas", steps, sched->num_steps);
         return HD_ERR_UNSUPPORTED;
     }
-    if (scratch_bytes < hd_denoise_run_scratch_bytes(B, S, I, steps)) {
+    // a separate unconditional sequence: x_pred rows for the longer of the two
+    const int S_rows = u && u->S > S ? u->S : S;
+    if (scratch_bytes < hd_denoise_run_scratch_bytes(B, S_rows, I, steps)) {
         hd_set_error("denoise: scratch too small");
         return HD_ERR_OOM;
     }
     const int64_t n = (int64_t)I_t * 3072;
     char *p = (char *)scratch;
     uint16_t *vin = (uint16_t *)p; p += al256((int64_t)B * I * 3072 * 2);
-    uint16_t *xp = (uint16_t *)p; p += al256((int64_t)B * S * 3072 * 2);
+    uint16_t *xp = (uint16_t *)p; p += al256((int64_t)B * S_rows * 3072 * 2);
+    uint16_t *xp_u = xp + (size_t)S_rows * 3072;
     float *mo_c = (float *)p, *mo_u = mo_c + n, *mo = mo_u + n; p += al256(3 * n * 4);
     float *st = (float *)p; p += al256(7 * n * 4);
     float *tdev = (float *)p;
@@ -658,7 +672,7 @@ static hd_status denoise_loop(const hd_forward_binding *bw, hd_forward_workspace
                 status = HD_ERR_IO;
             }
             vptr = vin;
-        } else if (B == 2) {
+        } else if (B == 2 && !u) {
             for (int b = 0; b < 2 && status == HD_OK; b++)
                 if (hipMemcpyAsync(vin + b * n, z, n * 2, hipMemcpyDeviceToDevice, hs) != hipSuccess) {
                     hd_set_error("denoise: latent copy failed");
@@ -670,16 +684,24 @@ static hd_status denoise_loop(const hd_forward_binding *bw, hd_forward_workspace
         if (B == 1 && (vis || mask || n_ref))
             status = hd_forward(bw, ws, ids, T, pos, mask, vptr, I, vis, tdev + i, nullptr, S, H, KV,
                                 HID, FF, D, tms, nullptr, xp, nullptr);
+        else if (u)   // cond and uncond as two sequences of their own lengths
+            status = hd_forward_batched(bw, ws, 1, ids, T, pos, ar_len, z, I, tdev + (size_t)B * i,
+                                        S, H, KV, HID, FF, D, tms, nullptr, xp, nullptr);
         else
             status = hd_forward_batched(bw, ws, B, ids, T, pos, ar_len, vptr, I,
                                         tdev + (size_t)B * i, S, H, KV, HID, FF, D, tms, nullptr, xp,
                                         nullptr);
+        if (status == HD_OK && u)
+            status = hd_forward_batched(bw, u->ws, 1, u->ids, u->T, u->pos, u->ar_len, z, I,
+                                        tdev + (size_t)B * i + 1, u->S, H, KV, HID, FF, D, tms,
+                                        nullptr, xp_u, nullptr);
         if (status != HD_OK) break;
         hd_cuda_clear_error();
         hd_sched_vcond(z, xp + (size_t)T * 3072, sg, mo_c, (int)n);
         const float *m = mo_c;
         if (B == 2) {
-            hd_sched_vcond(z, xp + ((size_t)S + T) * 3072, sg, mo_u, (int)n);
+            const uint16_t *xu = u ? xp_u + (size_t)u->T * 3072 : xp + ((size_t)S + T) * 3072;
+            hd_sched_vcond(z, xu, sg, mo_u, (int)n);
             hd_sched_cfg_guided(mo_c, mo_u, guidance, mo, (int)n);
             m = mo;
         }
@@ -761,6 +783,44 @@ extern "C" hd_status hd_denoise(const hd_forward_binding *bw, hd_forward_workspa
     return denoise_loop(bw, ws, sampler, sched, steps, B, ids, T, pos, ar_len, nullptr, nullptr, z,
                         I, nullptr, 0, guidance, seed, sn_start, sn_end, clip, S, H, KV, HID, FF, D,
                         tms, scratch, scratch_bytes, stream);
+}
+
+extern "C" int64_t hd_denoise_cfg_scratch_bytes(int seq, int seq_uncond, int img_tokens,
+                                                int steps) {
+    return hd_denoise_run_scratch_bytes(2, seq > seq_uncond ? seq : seq_uncond, img_tokens, steps);
+}
+
+extern "C" hd_status hd_denoise_cfg(const hd_forward_binding *bw, hd_forward_workspace *ws,
+                                    hd_forward_workspace *ws_uncond, int sampler,
+                                    const hd_scheduler *sched, int steps, const int64_t *ids, int T,
+                                    const float *pos, int ar_len, int S, const int64_t *ids_uncond,
+                                    int T_uncond, const float *pos_uncond, int ar_len_uncond,
+                                    int S_uncond, void *z, int I, float guidance, uint64_t seed,
+                                    float sn_start, float sn_end, float clip, int H, int KV,
+                                    int HID, int FF, int D, int tms, void *scratch,
+                                    int64_t scratch_bytes, void *stream) {
+    if (!bw || !ws || !ws_uncond || !sched || !ids || !pos || !ids_uncond || !pos_uncond || !z ||
+        !scratch || I <= 0 || steps < 1) {
+        hd_set_error("denoise_cfg: null argument");
+        return HD_ERR_MISSING;
+    }
+    if (sampler < HD_SAMPLER_EULER || sampler > HD_SAMPLER_UNIPC) {
+        hd_set_error("denoise_cfg: sampler must be 0..2");
+        return HD_ERR_UNSUPPORTED;
+    }
+    if (T + I != S || T_uncond + I != S_uncond || T_uncond < 1) {
+        hd_set_error("denoise_cfg: text + image tokens != seq (cond %d + %d vs %d, uncond %d + %d vs %d)",
+                     T, I, S, T_uncond, I, S_uncond);
+        return HD_ERR_MISMATCH;
+    }
+    if (ws_uncond == ws) {
+        hd_set_error("denoise_cfg: the unconditional sequence needs its own workspace");
+        return HD_ERR_MISMATCH;
+    }
+    const UncondSeq u{ws_uncond, ids_uncond, T_uncond, ar_len_uncond, S_uncond, pos_uncond};
+    return denoise_loop(bw, ws, sampler, sched, steps, 2, ids, T, pos, ar_len, nullptr, nullptr, z,
+                        I, nullptr, 0, guidance, seed, sn_start, sn_end, clip, S, H, KV, HID, FF, D,
+                        tms, scratch, scratch_bytes, stream, &u);
 }
 
 extern "C" hd_status hd_denoise_visual(const hd_forward_binding *bw, hd_forward_workspace *ws,

@@ -335,6 +335,12 @@ SIGNATURES = {
                            ctypes.POINTER(hd_scheduler), c_int, c_int, P, c_int, P, c_int, P, c_int,
                            c_float, ctypes.c_uint64, c_float, c_float, c_float, c_int, c_int, c_int,
                            c_int, c_int, c_int, c_int, P, c_int64, P]),
+    "hd_denoise_cfg_scratch_bytes": (c_int64, [c_int, c_int, c_int, c_int]),
+    "hd_denoise_cfg": (c_int, [ctypes.POINTER(hd_forward_binding), ctypes.POINTER(hd_forward_workspace),
+                               ctypes.POINTER(hd_forward_workspace), c_int, ctypes.POINTER(hd_scheduler),
+                               c_int, P, c_int, P, c_int, c_int, P, c_int, P, c_int, c_int, P, c_int,
+                               c_float, ctypes.c_uint64, c_float, c_float, c_float, c_int, c_int, c_int,
+                               c_int, c_int, c_int, P, c_int64, P]),
     "hd_denoise_visual": (c_int, [ctypes.POINTER(hd_forward_binding), ctypes.POINTER(hd_forward_workspace),
                                   c_int, ctypes.POINTER(hd_scheduler), c_int, P, c_int, P, P,
                                   ctypes.POINTER(hd_visual_cond), P, c_int, P, c_int, ctypes.c_uint64,

@@ -1,6 +1,6 @@
 /*
  * CPU oracle of the o1 decoder-block hot path (TEST INFRASTRUCTURE ONLY; see
- * o1_oracle.h). fp32, OpenMP, a blocked SGEMM with an 8-wide vector
+ * o1_oracle.h). fp32, OpenMP, a packed-panel SGEMM with a 6 x 16 FMA
  * micro-kernel. Each function cites the reference code it restates.
  */
 #include "o1_oracle.h"
@@ -8,11 +8,11 @@
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
+#include <immintrin.h>
 #ifdef _OPENMP
 #include <omp.h>
 #endif
 
-typedef float v8f __attribute__((vector_size(32)));
 
 int o1o_num_threads(void) {
 #ifdef _OPENMP
@@ -47,58 +47,104 @@ static inline float rnd(float v, int r) { return r ? o1o_bf16_round(v) : v; }
 
 /* ------------------------------------------------------------------ */
 /* SGEMM y = x . w^T (both K-contiguous), gemm.cu:35-70 math in fp32.  */
+/* Packed-panel FMA kernel: 6 rows x 16 columns of C per call, B packed */
+/* K-major in panels of 16 columns, K in blocks of 256. Per output the  */
+/* products are accumulated in ascending k order.                      */
 /* ------------------------------------------------------------------ */
-static inline float hsum8(v8f v) {
-    return ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
+#define GM 6
+#define GN 16
+#define GKC 256
+#define GMC 96
+#define GNC 128
+
+/* acc[6][16] += Ap[kc][6] * Bp[kc][16] (both packed K-major). */
+static void kern6x16(int kc, const float *Ap, const float *Bp, float acc[GM][GN]) {
+    __m256 c[GM][2];
+    for (int i = 0; i < GM; i++) {
+        c[i][0] = _mm256_loadu_ps(acc[i]);
+        c[i][1] = _mm256_loadu_ps(acc[i] + 8);
+    }
+    for (int k = 0; k < kc; k++) {
+        const __m256 b0 = _mm256_loadu_ps(Bp + (size_t)k * GN);
+        const __m256 b1 = _mm256_loadu_ps(Bp + (size_t)k * GN + 8);
+        for (int i = 0; i < GM; i++) {
+            const __m256 av = _mm256_broadcast_ss(Ap + (size_t)k * GM + i);
+            c[i][0] = _mm256_fmadd_ps(av, b0, c[i][0]);
+            c[i][1] = _mm256_fmadd_ps(av, b1, c[i][1]);
+        }
+    }
+    for (int i = 0; i < GM; i++) {
+        _mm256_storeu_ps(acc[i], c[i][0]);
+        _mm256_storeu_ps(acc[i] + 8, c[i][1]);
+    }
 }
 
-/* 4 x 4 outputs over k in [0, K8) vector part, scalar tail. */
-static void micro4x4(const float *x, const float *w, int K, int ldx, int ldw, float out[4][4],
-                     int mr, int nr) {
-    v8f acc[4][4];
-    memset(acc, 0, sizeof(acc));
-    const int K8 = K & ~7;
-    const float *xr[4], *wr[4];
-    for (int i = 0; i < 4; i++) xr[i] = x + (size_t)(i < mr ? i : 0) * ldx;
-    for (int j = 0; j < 4; j++) wr[j] = w + (size_t)(j < nr ? j : 0) * ldw;
-    for (int k = 0; k < K8; k += 8) {
-        v8f a[4], b[4];
-        for (int i = 0; i < 4; i++) memcpy(&a[i], xr[i] + k, 32);
-        for (int j = 0; j < 4; j++) memcpy(&b[j], wr[j] + k, 32);
-        for (int i = 0; i < 4; i++)
-            for (int j = 0; j < 4; j++) acc[i][j] += a[i] * b[j];
-    }
-    for (int i = 0; i < 4; i++)
-        for (int j = 0; j < 4; j++) {
-            float s = hsum8(acc[i][j]);
-            for (int k = K8; k < K; k++) s += xr[i][k] * wr[j][k];
-            out[i][j] = s;
+/* C[m][n] (ldc) = sum_k A[m][k] * B(k, n) for one M x N tile, where
+ * B(k, n) = b[n * ldb + k] when bt (weights [N][K]) else b[k * ldb + n]
+ * (values [K][N]). Bp: scratch of GNC * GKC floats. */
+static void gemm_tile(const float *A, long lda, const float *b, long ldb, int bt, float *C, long ldc,
+                      int M, int N, int K, float *Bp) {
+    float Ap[GKC * GM];
+    for (int m = 0; m < M; m++) memset(C + (size_t)m * ldc, 0, sizeof(float) * N);
+    const int np = (N + GN - 1) / GN;
+    for (int k0 = 0; k0 < K; k0 += GKC) {
+        const int kc = K - k0 < GKC ? K - k0 : GKC;
+        for (int p = 0; p < np; p++) {
+            float *dst = Bp + (size_t)p * GKC * GN;
+            for (int j = 0; j < GN; j++) {
+                const int n = p * GN + j;
+                if (n >= N)
+                    for (int k = 0; k < kc; k++) dst[(size_t)k * GN + j] = 0.f;
+                else if (bt)
+                    for (int k = 0; k < kc; k++) dst[(size_t)k * GN + j] = b[(size_t)n * ldb + k0 + k];
+                else
+                    for (int k = 0; k < kc; k++) dst[(size_t)k * GN + j] = b[(size_t)(k0 + k) * ldb + n];
+            }
         }
+        for (int m = 0; m < M; m += GM) {
+            const int mr = M - m < GM ? M - m : GM;
+            for (int i = 0; i < GM; i++) {
+                const float *ar = A + (size_t)(m + (i < mr ? i : 0)) * lda + k0;
+                for (int k = 0; k < kc; k++) Ap[(size_t)k * GM + i] = ar[k];
+            }
+            for (int p = 0; p < np; p++) {
+                const int nr = N - p * GN < GN ? N - p * GN : GN;
+                float acc[GM][GN];
+                for (int i = 0; i < GM; i++)
+                    for (int j = 0; j < GN; j++)
+                        acc[i][j] = (i < mr && j < nr) ? C[(size_t)(m + i) * ldc + p * GN + j] : 0.f;
+                kern6x16(kc, Ap, Bp + (size_t)p * GKC * GN, acc);
+                for (int i = 0; i < mr; i++)
+                    for (int j = 0; j < nr; j++) C[(size_t)(m + i) * ldc + p * GN + j] = acc[i][j];
+            }
+        }
+    }
 }
 
 void o1o_linear(const float *x, const float *w, const float *bias, float *y, int M, int N, int K,
                 int mode) {
-    const int TB = 64;
-    const int tm = (M + TB - 1) / TB, tn = (N + TB - 1) / TB;
-#pragma omp parallel for schedule(dynamic, 1)
-    for (long t = 0; t < (long)tm * tn; t++) {
-        const int m0 = (int)(t / tn) * TB, n0 = (int)(t % tn) * TB;
-        const int m1 = m0 + TB < M ? m0 + TB : M, n1 = n0 + TB < N ? n0 + TB : N;
-        for (int m = m0; m < m1; m += 4)
-            for (int n = n0; n < n1; n += 4) {
-                float o[4][4];
-                int mr = m1 - m < 4 ? m1 - m : 4, nr = n1 - n < 4 ? n1 - n : 4;
-                micro4x4(x + (size_t)m * K, w + (size_t)n * K, K, K, K, o, mr, nr);
-                for (int i = 0; i < mr; i++)
-                    for (int j = 0; j < nr; j++) {
-                        float v = o[i][j];
-                        float b = bias ? bias[n + j] : 0.f;
-                        if (mode == 0) v = v + b;
-                        else if (mode == 1) v = o1o_bf16_round(v + b);
-                        else v = bias ? o1o_bf16_round(o1o_bf16_round(v) + b) : o1o_bf16_round(v);
-                        y[(size_t)(m + i) * N + n + j] = v;
-                    }
-            }
+    const int tm = (M + GMC - 1) / GMC, tn = (N + GNC - 1) / GNC;
+#pragma omp parallel
+    {
+        float *Bp = (float *)malloc(sizeof(float) * GNC * GKC);
+        float *C = (float *)malloc(sizeof(float) * GMC * GNC);
+#pragma omp for schedule(dynamic, 1)
+        for (long t = 0; t < (long)tm * tn; t++) {
+            const int m0 = (int)(t / tn) * GMC, n0 = (int)(t % tn) * GNC;
+            const int mb = M - m0 < GMC ? M - m0 : GMC, nb = N - n0 < GNC ? N - n0 : GNC;
+            gemm_tile(x + (size_t)m0 * K, K, w + (size_t)n0 * K, K, 1, C, GNC, mb, nb, K, Bp);
+            for (int i = 0; i < mb; i++)
+                for (int j = 0; j < nb; j++) {
+                    float v = C[(size_t)i * GNC + j];
+                    float bb = bias ? bias[n0 + j] : 0.f;
+                    if (mode == 0) v = v + bb;
+                    else if (mode == 1) v = o1o_bf16_round(v + bb);
+                    else v = bias ? o1o_bf16_round(o1o_bf16_round(v) + bb) : o1o_bf16_round(v);
+                    y[(size_t)(m0 + i) * N + n0 + j] = v;
+                }
+        }
+        free(Bp);
+        free(C);
     }
 }
 
@@ -188,13 +234,15 @@ void o1o_apply_rotary(const float *x, const float *cosd, const float *sind, floa
 void o1o_attention(const float *q, const float *k, const float *v, const float *mask, int Hq,
                    int Hkv, int S, int D, int ar_len, float scale, int prob_mode, int round,
                    float *out) {
-    const int QB = 16;
+    const int QB = 48;
     const int nqb = (S + QB - 1) / QB;
     const int grp = Hq / Hkv;
 #pragma omp parallel
     {
         float *sc = (float *)malloc(sizeof(float) * QB * (size_t)S);
         float *acc = (float *)malloc(sizeof(float) * QB * (size_t)D);
+        float *Bp = (float *)malloc(sizeof(float) * GKC * (size_t)((D + GN - 1) / GN * GN > GNC
+                                                                       ? (D + GN - 1) / GN * GN : GNC));
 #pragma omp for schedule(dynamic, 1)
         for (long job = 0; job < (long)Hq * nqb; job++) {
             const int h = (int)(job / nqb), qb = (int)(job % nqb);
@@ -203,15 +251,11 @@ void o1o_attention(const float *q, const float *k, const float *v, const float *
             const float *qh = q + ((size_t)h * S + s0) * D;
             const float *kk = k + (size_t)kh * S * D;
             const float *vv = v + (size_t)kh * S * D;
-            for (int i = 0; i < nq; i += 4)
-                for (int t = 0; t < S; t += 4) {
-                    float o[4][4];
-                    int mr = nq - i < 4 ? nq - i : 4, nr = S - t < 4 ? S - t : 4;
-                    micro4x4(qh + (size_t)i * D, kk + (size_t)t * D, D, D, D, o, mr, nr);
-                    for (int a = 0; a < mr; a++)
-                        for (int b = 0; b < nr; b++) sc[(size_t)(i + a) * S + t + b] = o[a][b];
-                }
-            memset(acc, 0, sizeof(float) * QB * D);
+            /* raw scores Q K^T, key columns in chunks of GNC */
+            for (int t0 = 0; t0 < S; t0 += GNC) {
+                const int nt = S - t0 < GNC ? S - t0 : GNC;
+                gemm_tile(qh, D, kk + (size_t)t0 * D, D, 1, sc + t0, S, nq, nt, D, Bp);
+            }
             for (int i = 0; i < nq; i++) {
                 const int s = s0 + i;
                 float *row = sc + (size_t)i * S;
@@ -230,19 +274,24 @@ void o1o_attention(const float *q, const float *k, const float *v, const float *
                     sum += e;
                 }
                 const float inv = (float)(1.0 / sum);
-                float *ar = acc + (size_t)i * D;
                 for (int t = 0; t < lim; t++) {
                     float p = row[t] * inv;
                     if (prob_mode == 1) p = o1o_bf16_round(p);
-                    const float *vr = vv + (size_t)t * D;
-                    for (int d = 0; d < D; d++) ar[d] += p * vr[d];
+                    row[t] = p;
                 }
-                float *dst = out + ((size_t)s * Hq + h) * D;
+                for (int t = lim; t < S; t++) row[t] = 0.f;   /* masked keys */
+            }
+            /* P V: V [S][D] is already K-major */
+            gemm_tile(sc, S, vv, D, 0, acc, D, nq, D, S, Bp);
+            for (int i = 0; i < nq; i++) {
+                float *dst = out + ((size_t)(s0 + i) * Hq + h) * D;
+                const float *ar = acc + (size_t)i * D;
                 for (int d = 0; d < D; d++) dst[d] = rnd(ar[d], round);
             }
         }
         free(sc);
         free(acc);
+        free(Bp);
     }
 }
 

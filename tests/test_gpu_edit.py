@@ -149,3 +149,94 @@ def test_denoise_visual_argument_checks(pkg, lib):
     ws.xe_ref, ws.n_ref = 0x2000, 8
     assert call(ws, 8, 64, fake, 16, 88) == pkg.HD_ERR_MISMATCH          # cache of another size
     assert b"caches 8" in lib.hd_last_error()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cached", [True, False])
+def test_edit_forward_multi_reference_vs_oracle(pkg, lib, dev, cached):
+    """The edit configuration's layout at reduced width through hd_forward:
+    text rows at position 0 with image-pad rows (vision conditioning:
+    masked scatter + DeepStack into blocks 0-2) and the timestep token, the
+    target grid, then two reference grids at +64 and +128 rows
+    (hd_seq_grid_positions), full bidirectional attention; the references'
+    x_embedder rows cached in the workspace (forward.c:301-313) or computed
+    from the patches. Against the oracle's forward, which embeds every
+    image row itself (forward.c:253-397)."""
+    from tests.common import make_forward_weights, bf16, cosine
+    from tests.test_gpu_forward import store_names
+    from oracle import oracle as orc
+    nLf, Tf, gh, gw, R = 4, 24, 8, 8, 2
+    It = gh * gw
+    nref = R * It
+    I = It + nref
+    Sf = Tf + I
+    fw = make_forward_weights(nLf, HID, H, KV, FF, D, seed=61)
+    rng = np.random.default_rng(62)
+    ids = rng.integers(0, 151643, Tf).astype(np.int64)
+    vrows = [2, 3, 4, 5, 6, 7, 8, 9]
+    ids[vrows] = IMG_PAD
+    ids[-1] = TMS
+    vmask = np.zeros(Sf, np.uint8)
+    vmask[vrows] = 1
+    g = torch.Generator().manual_seed(63)
+    emb = bf16(torch.randn(len(vrows), HID, generator=g))
+    dsl = [bf16(torch.randn(len(vrows), HID, generator=g) * 0.5) for _ in range(3)]
+    vin = bf16(torch.from_numpy(rng.standard_normal((I, 3072)).astype(np.float32))).numpy()
+    pos = np.zeros((3, Sf), np.float32)
+    segs = 1 + R
+    arr = lambda v: (ctypes.c_int * segs)(*v)
+    assert lib.hd_seq_grid_positions(Tf, segs, arr([gh] * segs), arr([gw] * segs),
+                                     arr([64 * k for k in range(segs)]), None, 0.0, pkg.np_ptr(pos)) == Sf
+    assert pos[1, Tf + It] == 64 and pos[1, Tf + 2 * It] == 128 and pos[2, Tf + It + 1] == 1
+    t = 0.42
+    pkg.set_block_config(theta=1e4)
+    tens = {k: v.to(dev, torch.bfloat16) for k, v in store_names(fw).items()}
+    store = pkg.WeightStore(tens)
+    fb = pkg.hd_forward_binding()
+    pkg.check_status(lib.hd_forward_resolve(ctypes.byref(store.store), nLf, ctypes.byref(fb)), "resolve")
+    wsbuf = torch.empty(lib.hd_forward_workspace_bytes(Sf, I, H, KV, HID, FF, D, None),
+                        dtype=torch.uint8, device=dev)
+    ws = pkg.hd_forward_workspace()
+    ws.hidden_a = wsbuf.data_ptr()
+    vind = torch.from_numpy(vin).to(dev, torch.bfloat16)
+    if cached:
+        xe = _cache_refs_n(pkg, lib, dev, fb, vind[It:].contiguous(), nref)
+        ws.xe_ref, ws.n_ref = xe.data_ptr(), nref
+    embd, dsd = emb.to(dev, torch.bfloat16), [d.to(dev, torch.bfloat16) for d in dsl]
+    vmd = torch.from_numpy(vmask).to(dev)
+    vc = pkg.hd_visual_cond()
+    vc.image_embeds = embd.data_ptr()
+    for j in range(3):
+        vc.deepstack[j] = dsd[j].data_ptr()
+    vc.visual_mask = vmd.data_ptr()
+    vc.v_tokens = len(vrows)
+    idsd, posd = torch.from_numpy(ids).to(dev), torch.from_numpy(pos).to(dev)
+    td = torch.tensor([t], dtype=torch.float32, device=dev)
+    out = torch.empty(Sf, 3072, dtype=torch.bfloat16, device=dev)
+    st = lib.hd_forward(ctypes.byref(fb), ctypes.byref(ws), pkg.ptr(idsd), Tf, pkg.ptr(posd), None,
+                        pkg.ptr(vind), I, ctypes.addressof(vc), pkg.ptr(td), None, Sf, H, KV, HID,
+                        FF, D, TMS, None, pkg.ptr(out), None)
+    pkg.check_status(st, "hd_forward edit layout")
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    lib.hd_forward_binding_free(ctypes.byref(fb))
+    ofw = {k: v.numpy() for k, v in fw.items() if k != "blocks"}
+    ofw["blocks"] = [{k: v.numpy() for k, v in b.items()} for b in fw["blocks"]]
+    cfg = orc.block_cfg(H, KV, HID, FF, D, theta=1e4, faithful=0)
+    ref = orc.forward(ofw, cfg, ids, vin, t, pos, TMS,
+                      visual=(emb.numpy(), [d.numpy() for d in dsl], vmask))
+    r, c = rel_l2(got, ref), cosine(got, ref)
+    print(f"edit forward (cached={cached}): rel_l2={r:.3e} cos={c:.7f}", flush=True)
+    assert r <= 1e-2 and c >= 0.9999
+    # the target rows (the ones the sampler reads) hold the bound on their own
+    rt, ct = rel_l2(got[Tf:Tf + It], ref[Tf:Tf + It]), cosine(got[Tf:Tf + It], ref[Tf:Tf + It])
+    assert rt <= 1e-2 and ct >= 0.9999, (rt, ct)
+
+
+def _cache_refs_n(pkg, lib, dev, bw, ref, n):
+    stg = torch.empty(n, 1024, dtype=torch.bfloat16, device=dev)
+    xe = torch.empty(n, HID, dtype=torch.bfloat16, device=dev)
+    lib.hd_linear(pkg.ptr(ref), bw.xe1_w, None, pkg.ptr(stg), n, 1024, 3072, 1)
+    lib.hd_linear(pkg.ptr(stg), bw.xe2_w, bw.xe2_b, pkg.ptr(xe), n, HID, 1024, 1)
+    pkg.check_prim("x_embedder cache")
+    return xe
