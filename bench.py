@@ -56,6 +56,10 @@ def main():
     ap.add_argument("--config", default="c1", choices=sorted(CFGS))
     ap.add_argument("--layers", type=int, default=L)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-c2", action="store_true",
+                    help="with the default configuration 1, skip the configuration 2 (2048^2) timing "
+                         "that the same run adds as its `c2` object")
+    ap.add_argument("--c2-steps", type=int, default=10)
     ap.add_argument("--kernel-iters", type=int, default=20)
     ap.add_argument("--flash-only", action="store_true",
                     help="run only the flash attention kernel at the configuration's shape "
@@ -122,6 +126,66 @@ def main():
     model = synth.Model(tensors, args.layers)
     pkg.set_block_config(theta=1e4)          # 2D RoPE, theta 1e4 (synthetic benchmark configurations)
 
+    r = time_config(pkg, lib, synth, model, tensors, args.config, args.steps, args.warmup,
+                    args.layers, args.kernel_iters, dev, args)
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(S, T, gh, gw, B, args.layers)
+    metric = {"c0": "DiT block forwards/sec (config 0)",
+              "c1": "DiT denoise steps/sec (1024^2, CFG batch 2, 36 blocks)",
+              "c2": "DiT denoise steps/sec (2048^2, 36 blocks)",
+              "c3": "DiT edit steps/sec (1024^2 target + 3 references, 36 blocks)",
+              "c4": "DiT denoise steps/sec (1024^2, CFG batch 2) + LoRA merge and 28-step image"}
+    res = {
+        "metric": metric[args.config],
+        "value": round(1000.0 / r["ms"], 4),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms"], 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init bf16 weights seed 0, N(0,1) latents seed 42)",
+        "config": {"workload": cfg["name"], "batch": B, "seq_len": S, "image_tokens": I,
+                   "text_tokens": T, "layers": args.layers, "hidden": HID, "heads": NH,
+                   "kv_heads": NKV, "ffn": FF, "parallelism": "single GPU"},
+        "step_tflops": r["step_tflops"],
+        "step_mfma_frac": r["step_mfma_frac"],
+        "wall_s": r["wall_s"],
+        "roofline": dict(r["gemm"], traffic=read_traffic(args.config)),
+        "attention": r["attention"],
+        "cpu_baseline": cpu,
+    }
+    res.update(r["extra"])
+    if args.config == "c1" and not args.no_c2:
+        # the north-star configuration in the same run, on the same weights:
+        # 2048^2, 16384 image + 256 text tokens, batch 1
+        print("[bench] configuration 2 (2048^2) on the same model", file=sys.stderr, flush=True)
+        r2 = time_config(pkg, lib, synth, model, tensors, "c2", args.c2_steps, min(args.warmup, 3),
+                         args.layers, args.kernel_iters, dev, args)
+        c2 = CFGS["c2"]
+        res["c2"] = {"workload": c2["name"], "seq_len": c2["text"] + c2["gh"] * c2["gw"], "batch": 1,
+                     "steps": args.c2_steps, "ms_per_step": round(r2["ms"], 3),
+                     "steps_per_s": round(1000.0 / r2["ms"], 4), "step_tflops": r2["step_tflops"],
+                     "step_mfma_frac": r2["step_mfma_frac"], "wall_s": r2["wall_s"],
+                     "gemm": dict(r2["gemm"], traffic=read_traffic("c2")), "attention": r2["attention"]}
+    print(json.dumps(res))
+
+
+def time_config(pkg, lib, synth, model, tensors, name, steps, warmup, layers, kernel_iters, dev, args):
+    """Times `steps` denoiser steps of configuration `name` on `model`
+    (untimed `warmup` steps first), then the step's dominant GEMM (gate/up +
+    SwiGLU at M = B*S) and its attention launch alone, each over
+    `kernel_iters` launches between HIP events on the library's stream."""
+    import numpy as np
+    import torch
+    cfg = CFGS[name]
+    B, T, gh, gw, R = cfg["batch"], cfg["text"], cfg["gh"], cfg["gw"], cfg["refs"]
+    I = gh * gw * (1 + R)
+    S = T + I
     # synthetic inputs: text ids (last = timestep token), latents N(0,1) seed 42
     g = torch.Generator().manual_seed(42)
     lat = torch.randn(I, 3072, generator=g)
@@ -156,7 +220,7 @@ def main():
                             tensors["model.x_embedder.proj2.bias"])
         ws.xe_ref = xe_ref.data_ptr()
         ws.n_ref = n_ref
-    if args.config == "c4":
+    if name == "c4":
         extra = run_c4(pkg, lib, model, tensors, cfg, ws, ids, posd, vin, T, I, S, dev, args)
     vis = None
     if R:
@@ -177,24 +241,24 @@ def main():
         if st != 0:
             raise RuntimeError(lib.hd_last_error().decode())
 
-    print("[bench] warmup", file=sys.stderr, flush=True)
-    for _ in range(args.warmup):
+    print(f"[bench] {name}: warmup", file=sys.stderr, flush=True)
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all(), "non-finite output"
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    print(f"[bench] timing {args.steps} steps", file=sys.stderr, flush=True)
+    print(f"[bench] {name}: timing {steps} steps", file=sys.stderr, flush=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     e0.record()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms = e0.elapsed_time(e1) / args.steps
-    steps_per_s = 1000.0 / ms
-    flops = step_flops(S, B, I, T) * args.layers / L if args.layers != L else step_flops(S, B, I, T)
+    ms = e0.elapsed_time(e1) / steps
+    flops = step_flops(S, B, I, T) * layers / L if layers != L else step_flops(S, B, I, T)
+    del wsbuf, out
 
     # ---- dominant kernel: gate/up GEMM with SwiGLU epilogue, timed alone ----
     M = B * S
@@ -207,14 +271,15 @@ def main():
     torch.cuda.synchronize()
     k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     k0.record()
-    for _ in range(args.kernel_iters):
+    for _ in range(kernel_iters):
         lib.hd_linear_swiglu(pkg.ptr(xln), ctypes.c_void_p(blk.gate_proj), ctypes.c_void_p(blk.up_proj),
                              pkg.ptr(swi), M, FF, HID)
     k1.record()
     torch.cuda.synchronize()
-    kms = k0.elapsed_time(k1) / args.kernel_iters
+    kms = k0.elapsed_time(k1) / kernel_iters
     kflop = 2.0 * M * (2 * FF) * HID
     achieved = kflop / (kms * 1e-3) / 1e12
+    del xln, swi
 
     # attention kernel alone (flash, full non-causal) at the step's shape
     # N(0,1) operands, V included: matrix-core power (and so the clock the
@@ -236,54 +301,27 @@ def main():
         attn()
     torch.cuda.synchronize()
     k0.record()
-    for _ in range(args.kernel_iters):
+    for _ in range(kernel_iters):
         attn()
     k1.record()
     torch.cuda.synchronize()
-    ams = k0.elapsed_time(k1) / args.kernel_iters
+    ams = k0.elapsed_time(k1) / kernel_iters
     aflop = 4.0 * B * S * S * NH * D
     attn_tf = aflop / (ams * 1e-3) / 1e12
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        cpu = cpu_baseline(S, T, gh, gw, B, args.layers)
-
-    metric = {"c0": "DiT block forwards/sec (config 0)",
-              "c1": "DiT denoise steps/sec (1024^2, CFG batch 2, 36 blocks)",
-              "c2": "DiT denoise steps/sec (2048^2, 36 blocks)",
-              "c3": "DiT edit steps/sec (1024^2 target + 3 references, 36 blocks)",
-              "c4": "DiT denoise steps/sec (1024^2, CFG batch 2) + LoRA merge and 28-step image"}
-    res = {
-        "metric": metric[args.config],
-        "value": round(steps_per_s, 4),
-        "unit": "steps/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 3),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (random-init bf16 weights seed 0, N(0,1) latents seed 42)",
-        "config": {"workload": cfg["name"], "batch": B, "seq_len": S, "image_tokens": I,
-                   "text_tokens": T, "layers": args.layers, "hidden": HID, "heads": NH,
-                   "kv_heads": NKV, "ffn": FF, "parallelism": "single GPU"},
+    del q, kk, vt, ao, fws
+    return {
+        "ms": ms, "wall_s": round(wall, 3),
         "step_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
         "step_mfma_frac": round(flops / (ms * 1e-3) / PEAK_BF16, 4),
-        "wall_s": round(wall, 3),
-        "roofline": {"kernel": "gemm_bf16 gate/up + SwiGLU epilogue", "bound": "mfma",
-                     "achieved": round(achieved, 1), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved * 1e12 / PEAK_BF16, 4),
-                     "traffic": read_traffic() if args.config in ("c1", "c4") else None,
-                     "launch_ms": round(kms, 4), "shape": [M, 2 * FF, HID]},
-        "attention": {"kernel": "flash_fwd (full, GQA 32/8, D=128; tail-split workspace as in the block)", "achieved": round(attn_tf, 1),
-                      "unit": "TFLOP/s", "frac": round(attn_tf * 1e12 / PEAK_BF16, 4),
-                      "launch_ms": round(ams, 4)},
-        "cpu_baseline": cpu,
+        "gemm": {"kernel": "gemm_bf16 gate/up + SwiGLU epilogue", "bound": "mfma",
+                 "achieved": round(achieved, 1), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+                 "frac": round(achieved * 1e12 / PEAK_BF16, 4), "launch_ms": round(kms, 4),
+                 "shape": [M, 2 * FF, HID]},
+        "attention": {"kernel": "flash_fwd (full, GQA 32/8, D=128; tail-split workspace as in the block)",
+                      "achieved": round(attn_tf, 1), "unit": "TFLOP/s",
+                      "frac": round(attn_tf * 1e12 / PEAK_BF16, 4), "launch_ms": round(ams, 4)},
+        "extra": extra,
     }
-    res.update(extra)
-    print(json.dumps(res))
 
 
 def run_c0(pkg, lib, cfg, args, dev):
@@ -600,11 +638,12 @@ def elementwise_bench(pkg, lib, iters):
     print(json.dumps({"elementwise": rows, "peak_GB_s": PEAK_HBM / 1e9}))
 
 
-def read_traffic():
-    """HBM bytes per launch of the dominant kernel, from the committed counter
-    summary (two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled by
-    a 1 GiB copy's counters); None when absent."""
-    path = os.path.join(ROOT, "profiles", "gemm_swiglu_c1_traffic.txt")
+def read_traffic(config):
+    """HBM bytes per launch of the dominant kernel at `config`'s shape, from
+    the committed counter summary (two rocprofv3 --pmc passes, FETCH_SIZE and
+    WRITE_SIZE, scaled by a 1 GiB copy's counters); None when absent."""
+    name = {"c4": "c1"}.get(config, config)
+    path = os.path.join(ROOT, "profiles", f"gemm_swiglu_{name}_traffic.txt")
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_launch:"):
@@ -614,12 +653,30 @@ def read_traffic():
     return None
 
 
+def host_cpu():
+    """Threads this process may run on (nproc), the CPU model, and the
+    OpenMP thread count the baseline uses (all of them)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    model = platform.processor() or platform.machine()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return n, model
+
+
 def cpu_lora_baseline(r, welems):
     """The fp32 C oracle merging one gate-sized target (12288 x 4096, rank r)
     on the host cores, extrapolated by element count to the whole merge."""
     import numpy as np
     from oracle import oracle as orc
-    threads = min(os.cpu_count() or 1, 16)
+    threads, model = host_cpu()
     orc.lib().o1o_set_threads(threads)
     N, K = FF, HID
     rng = np.random.default_rng(0)
@@ -630,9 +687,10 @@ def cpu_lora_baseline(r, welems):
     orc.lora_merge(w, up, down, 1.0)
     dt = time.perf_counter() - t0
     return {"value": round(dt * 1e3 * welems / (N * K), 1), "unit": "ms (whole merge)", "cores": threads,
-            "kind": "port",
+            "kind": "port", "nproc": threads, "cpu_model": model,
+            "omp_threads": orc.lib().o1o_num_threads(),
             "sample": f"1 target {N}x{K} rank {r} merged by the fp32 C oracle (OpenMP) in {dt:.2f}s, "
-                      f"x {welems / (N * K):.1f} for all targets; cpu={platform.processor() or platform.machine()}"}
+                      f"x {welems / (N * K):.1f} for all targets"}
 
 
 def cpu_baseline(S, T, gh, gw, B, layers):
@@ -642,7 +700,7 @@ def cpu_baseline(S, T, gh, gw, B, layers):
     import torch
     from oracle import oracle as orc
     from tests.common import make_block_weights, grid_pos, bf16
-    threads = min(os.cpu_count() or 1, 16)
+    threads, model = host_cpu()
     orc.lib().o1o_set_threads(threads)
     w = {k: v.numpy() for k, v in make_block_weights(HID, NH, NKV, FF, D, seed=0).items()}
     x = bf16(torch.randn(S, HID, generator=torch.Generator().manual_seed(1))).numpy()
@@ -652,10 +710,11 @@ def cpu_baseline(S, T, gh, gw, B, layers):
     orc.decoder_block(x, pos, w, cfg)
     dt = time.perf_counter() - t0
     return {"value": round(1.0 / (dt * layers * B), 6), "unit": "steps/s", "cores": threads,
-            "kind": "port",
-            "sample": f"1 decoder block, 1 sequence of S={S} (fp32 C oracle, OpenMP); "
-                      f"steps/s = 1/(t_block x {layers} blocks x {B} CFG sequences); "
-                      f"t_block={dt:.2f}s; cpu={platform.processor() or platform.machine()}"}
+            "kind": "port", "nproc": threads, "cpu_model": model,
+            "omp_threads": orc.lib().o1o_num_threads(),
+            "sample": f"1 decoder block, 1 sequence of S={S} (fp32 C oracle: packed-panel AVX2 FMA "
+                      f"SGEMM, OpenMP on every host thread); steps/s = 1/(t_block x {layers} blocks x "
+                      f"{B} CFG sequences), a labelled extrapolation; t_block={dt:.2f}s"}
 
 
 if __name__ == "__main__":
