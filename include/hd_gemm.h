@@ -72,6 +72,18 @@ void hd_linear_residual_ws(const void *x_dev, const void *w_dev, const void *res
 /* Workspace bytes that let every tail split of the current device run. */
 int64_t hd_gemm_ws_bytes(void);
 
+/* hd_linear_noalloc: no counterpart in the reference. For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): hd_linear_ws with the tail-split
+ * workspace in a static device array of hd_linear_noalloc_scratch_bytes()
+ * (80 MiB, one copy per GPU, held until the process ends) instead of a
+ * workspace argument. Allocates nothing. Errors (hd_cuda_last_error) when
+ * the current device's tail split needs more than the array holds. Calls
+ * that overlap on one GPU share the array and race. */
+void hd_linear_noalloc(const void *x_dev, const void *w_dev, const void *bias_dev, void *y_dev,
+                       int M, int N, int K);
+int64_t hd_linear_noalloc_scratch_bytes(void);
+
 /* ---- fused-epilogue entry points (extension) --------------------------
  * y = bf16(res + bf16(x . W^T))      : residual epilogue (o_proj, down)   */
 void hd_linear_residual(const void *x_dev, const void *w_dev,

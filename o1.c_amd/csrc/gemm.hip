@@ -1611,6 +1611,53 @@ extern "C" void hd_linear_ws(const void *x, const void *w, const void *bias, voi
     hd_check_launch("linear");
 }
 
+// ---- hd_linear_noalloc: hd_linear_ws with the tail-split workspace in a
+// file-scope device array, for callers that cannot allocate (code under
+// graph capture, serving loops, harnesses that forbid hipMalloc). 80 MiB:
+// the workspace hd_gemm_ws_bytes() asks for on a 256-CU device (256 fp32
+// 256x256 partial tiles + 128 bf16 staging tiles). Each GPU the library runs
+// on holds its own copy until the process ends. Every call on a device
+// shares that device's array: calls that overlap on one GPU (two streams,
+// two threads) race. The split partials are written in full before the
+// merge reads them, so nothing in the array has to start at zero.
+static constexpr int64_t kNoAllocScratchBytes = (int64_t)256 * 256 * 256 * 4 + 128 * 256 * 256 * 2;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+static constexpr int kMaxDevices = 64;
+static void *g_scratch_dev[kMaxDevices];   // the array's device address, per device
+
+extern "C" int64_t hd_linear_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" void hd_linear_noalloc(const void *x, const void *w, const void *bias, void *y, int M,
+                                  int N, int K) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        snprintf(hd_cuda_errbuf(), 512, "linear_noalloc: no current device (or device id >= %d)",
+                 kMaxDevices);
+        return;
+    }
+    if (!g_scratch_dev[dev]) {
+        // once per device, with that device current: the host-side name of
+        // the array is not its device address
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            snprintf(hd_cuda_errbuf(), 512, "linear_noalloc: hipGetSymbolAddress(scratch): %s",
+                     hipGetErrorString(e));
+            return;
+        }
+        g_scratch_dev[dev] = p;
+    }
+    const int64_t need = hd_gemm_ws_bytes();
+    if (need > kNoAllocScratchBytes) {
+        snprintf(hd_cuda_errbuf(), 512,
+                 "linear_noalloc: this device's tail split needs %lld workspace bytes, the static "
+                 "scratch holds %lld",
+                 (long long)need, (long long)kNoAllocScratchBytes);
+        return;
+    }
+    hd_linear_ws(x, w, bias, y, M, N, K, g_scratch_dev[dev], kNoAllocScratchBytes);
+}
+
 // hd_linear writing rows of stride ldc (>= N, ldc % 8 == 0): the vision
 // tower's fc1 lands in a row padded to the next GEMM's K.
 extern "C" void hd_linear_ld(const void *x, const void *w, const void *bias, void *y, int M, int N,

@@ -385,6 +385,8 @@ SIGNATURES = {
     "hd_linear_ws": (None, [P, P, P, P, c_int, c_int, c_int, P, ctypes.c_int64]),
     "hd_linear_residual_ws": (None, [P, P, P, P, c_int, c_int, c_int, P, ctypes.c_int64]),
     "hd_gemm_ws_bytes": (ctypes.c_int64, []),
+    "hd_linear_noalloc": (None, [P, P, P, P, c_int, c_int, c_int]),
+    "hd_linear_noalloc_scratch_bytes": (ctypes.c_int64, []),
     "hd_unipc_predict": (None, [P, P, P] + [c_float] * 7 + [c_int, P, c_int]),
 }
 
