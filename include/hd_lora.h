@@ -79,6 +79,11 @@ const char *hd_lora_last_error(void);
  * rank above 256, HD_ERR_RUNTIME on a launch failure. */
 hd_status hd_lora_merge_gpu(hd_lora_entry *entries, size_t count, void *stream);
 
+/* Extension: 0 = the merge kernel with its rank loop unrolled (default),
+ * 1 = the rolled loop, for same-process timing comparisons; identical
+ * results. Returns the previous setting. */
+int hd_lora_set_family(int family);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,7 +10,7 @@
 #include "../../include/hd_hip.h"
 #include "../../include/hd_lora.h"
 
-// A block owns a 128 x 128 tile of W; the rank
+// A block owns a 128 x 128 tile of W (two blocks per CU); the rank
 // product runs on v_mfma_f32_32x32x2_f32 (fp32 products, fp32 accumulation,
 // as an SGEMM does). Wave w computes rows [32w, 32w+32) x all 128 columns
 // (4 accumulators); MFMA A = up (row = output row), B = down (column = output
@@ -22,7 +22,8 @@
 #define LM_SD (LM_RC * (LM_T + 32))         // down slice [r][col], +32: the half-waves read
                                             // consecutive r rows in opposite bank halves
 #define LM_ST (LM_T * (LM_T + 8))           // fp32 delta tile [row][col] for the W update
-__global__ __launch_bounds__(256) void lora_merge_mfma_kernel(uint16_t *__restrict__ w,
+template <int OCC, bool UNROLL = true>
+__global__ __launch_bounds__(256, OCC) void lora_merge_mfma_kernel(uint16_t *__restrict__ w,
                                                               const float *__restrict__ up,
                                                               const float *__restrict__ down, int N,
                                                               int K, int R, float scale) {
@@ -77,13 +78,21 @@ __global__ __launch_bounds__(256) void lora_merge_mfma_kernel(uint16_t *__restri
             }
         }
         __syncthreads();
-        for (int r = 0; r < rc; r += 2) {
+        auto step = [&](int r) {
             const float a = su[(wave * 32 + l32) * (LM_RC + 1) + r + lh];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const float b = sd[(r + lh) * (LM_T + 32) + j * 32 + l32];
                 acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[j], 0, 0, 0);
             }
+        };
+        if (UNROLL && rc == LM_RC) {
+            // unrolled: the operand reads of later steps issue ahead of the
+            // MFMAs instead of one LDS round trip per step
+#pragma unroll
+            for (int r = 0; r < LM_RC; r += 2) step(r);
+        } else {
+            for (int r = 0; r < rc; r += 2) step(r);
         }
         __syncthreads();
     }
@@ -122,6 +131,15 @@ __global__ __launch_bounds__(256) void lora_merge_mfma_kernel(uint16_t *__restri
     }
 }
 
+// hd_lora_set_family: 0 = the unrolled rank loop (default), 1 = the rolled
+// loop (same-process comparisons; identical results)
+static int g_lora_family = 0;
+extern "C" int hd_lora_set_family(int family) {
+    const int prev = g_lora_family;
+    g_lora_family = family == 1 ? 1 : 0;
+    return prev;
+}
+
 extern "C" hd_status hd_lora_merge_gpu(hd_lora_entry *entries, size_t count, void *stream) {
     if (count == 0) return HD_OK;
     if (!entries) {
@@ -143,8 +161,12 @@ extern "C" hd_status hd_lora_merge_gpu(hd_lora_entry *entries, size_t count, voi
         const int N = (int)e->out_dim, K = (int)e->in_dim, R = (int)e->rank;
         const float scale = e->multiplier * e->alpha / (float)e->rank;   // lora_merge.cu:54
         dim3 grid(hd_cdiv(K, LM_T), hd_cdiv(N, LM_T));
-        lora_merge_mfma_kernel<<<grid, 256, 0, st>>>((uint16_t *)e->base_dev, (const float *)e->up_dev,
-                                                     (const float *)e->down_dev, N, K, R, scale);
+        if (g_lora_family == 1)
+            lora_merge_mfma_kernel<2, false><<<grid, 256, 0, st>>>((uint16_t *)e->base_dev, (const float *)e->up_dev,
+                                                            (const float *)e->down_dev, N, K, R, scale);
+        else
+            lora_merge_mfma_kernel<2><<<grid, 256, 0, st>>>((uint16_t *)e->base_dev, (const float *)e->up_dev,
+                                                            (const float *)e->down_dev, N, K, R, scale);
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) {
             hd_set_error("lora: merge launch failed: %s", hipGetErrorString(err));

@@ -300,6 +300,7 @@ SIGNATURES = {
                                    c_int, c_int, c_int, c_int, ctypes.POINTER(hd_forward_diagnostics), P, P]),
     # hd_lora.h
     "hd_lora_merge_gpu": (c_int, [ctypes.POINTER(hd_lora_entry), c_size_t, P]),
+    "hd_lora_set_family": (c_int, [c_int]),
     "hd_lora_apply": (c_int, [ctypes.POINTER(hd_lora_config), ctypes.POINTER(hd_weight_store), c_int]),
     "hd_lora_last_error": (c_char_p, []),
     # hd_host.h

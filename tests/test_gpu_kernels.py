@@ -232,6 +232,37 @@ def test_lora_merge(pkg, lib, dev):
     assert np.mean(host(wd) == ref) > 0.99
 
 
+@pytest.mark.parametrize("N,K", [(12288, 4096), (1024, 4096), (4096, 12288)])
+def test_lora_merge_real_shapes(pkg, lib, dev, N, K):
+    """The configuration-4 targets at their real shapes (gate/up 12288 x 4096,
+    k/v 1024 x 4096, down 4096 x 12288), rank 64, A and B ~ N(0, 0.01),
+    alpha = rank and multiplier 1 (scale 1): W' = bf16(W + s up.down)
+    (lora_merge.cu:35-104 in its documented form, hd_lora.h:11-13) against
+    the fp32 oracle; every weight within one bf16 step, > 99 % identical."""
+    R = 64
+    rng = np.random.default_rng(N + K)
+    w = orc.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 0.02)
+    up = (rng.standard_normal((N, R)) * 0.01).astype(np.float32)
+    down = (rng.standard_normal((R, K)) * 0.01).astype(np.float32)
+    wd = dbf(w, dev)
+    upd, dnd = torch.from_numpy(up).to(dev), torch.from_numpy(down).to(dev)
+    e = pkg.hd_lora_entry()
+    e.rank, e.in_dim, e.out_dim, e.alpha, e.multiplier = R, K, N, float(R), 1.0
+    e.down_dev, e.up_dev, e.base_dev = dnd.data_ptr(), upd.data_ptr(), wd.data_ptr()
+    print(f"lora merge {N}x{K} r={R}", flush=True)
+    assert lib.hd_lora_merge_gpu(ctypes.byref(e), 1, None) == 0
+    torch.cuda.synchronize()
+    got = host(wd)
+    ref = orc.lora_merge(w, up, down, 1.0)
+    same = float(np.mean(got == ref))
+    print(f"lora merge {N}x{K}: identical {same:.5f}, changed by the merge {np.mean(ref != w):.3f}")
+    # one bf16 step, plus an absolute floor of 1e-4 x RMS (2e-6 here, 1/40 of
+    # a bf16 step at the weights' scale) for sums that cancel to near zero,
+    # where the fp32 delta's summation order moves the bf16 exponent
+    assert close_bf16(got, ref, ulps=1, atol_rel=1e-4)
+    assert same > 0.9999
+
+
 def test_sched_and_patchify_bit_exact(pkg, lib, dev):
     rng = np.random.default_rng(4)
     n = 3 * 64 * 64
