@@ -45,11 +45,16 @@ int hd_sdpa_create_split(hd_sdpa_plan **out, int batch, int q_heads,
 /* hd_cudnn_sdpa.h:78 */
 int hd_sdpa_execute_split(hd_sdpa_plan *plan, const void *q, const void *k,
                           const void *v, void *out, void *stream);
-/* hd_cudnn_sdpa.h:83. which = 0: causal head rows [0, ar_len) only;
- * which = 1: every row with full (non-causal) attention. */
+/* hd_cudnn_sdpa.h:83. which = 0: causal head rows [0, ar_len) only, into
+ * the plan's staging buffer (`out` is left untouched, as the reference's
+ * pass 0 writes only its staged head); which = 1: every row of `out` with
+ * full (non-causal) attention. */
 int hd_sdpa_execute_split_pass(hd_sdpa_plan *plan, int which, const void *q,
                                const void *k, const void *v, void *out,
                                void *stream);
+/* Extension: the staging buffer pass 0 of a split plan writes, seq-major
+ * [batch, ar_len, q_heads, head_dim] bf16 (NULL for a non-split plan). */
+const void *hd_sdpa_plan_stage(const hd_sdpa_plan *plan);
 /* hd_cudnn_sdpa.h:94 */
 int hd_sdpa_create_prod(hd_sdpa_plan **out, int batch, int q_heads,
                         int kv_heads, int seq, int ar_len, int head_dim,

@@ -50,6 +50,7 @@ struct FaArgs {
     float scale_log2;      // scale * log2(e)
     float inv_scale;       // 1 / scale (mask values are added to raw scores)
     int out_seq_major;
+    int out_rows;          // rows per sequence in `out` (S, or fewer for a staging buffer)
     // tail split: blocks [0, n_whole) each run one (b, head, q tile) unit over
     // all keys; the units from n_whole on run as `split` chunks of the key
     // tiles each, writing unnormalised partials to `part` (merged afterwards)
@@ -288,9 +289,9 @@ __global__ __launch_bounds__(NWV * 64, 8 / NWV) void flash_fwd_kernel(FaArgs a) 
     if (my_q >= a.q_row_end) return;
     uint16_t *dst;
     if (a.out_seq_major)
-        dst = a.out + (((size_t)b * a.S + my_q) * a.Hq + hq) * FA_D;
+        dst = a.out + (((size_t)b * a.out_rows + my_q) * a.Hq + hq) * FA_D;
     else
-        dst = a.out + (((size_t)b * a.Hq + hq) * a.S + my_q) * FA_D;
+        dst = a.out + (((size_t)b * a.Hq + hq) * a.out_rows + my_q) * FA_D;
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
@@ -345,8 +346,8 @@ __global__ __launch_bounds__(256) void fa_merge_kernel(FaArgs a, int n_tail) {
     const int hk = lin % a.Hkv, b = lin / a.Hkv, hq = hk * group + g;
     const int my_q = qt * BQ + row;
     if (my_q >= a.q_row_end) return;
-    const size_t o = a.out_seq_major ? (((size_t)b * a.S + my_q) * a.Hq + hq) * FA_D + d
-                                     : (((size_t)b * a.Hq + hq) * a.S + my_q) * FA_D + d;
+    const size_t o = a.out_seq_major ? (((size_t)b * a.out_rows + my_q) * a.Hq + hq) * FA_D + d
+                                     : (((size_t)b * a.Hq + hq) * a.out_rows + my_q) * FA_D + d;
     a.out[o] = f2bf(acc * (1.0f / L));
 }
 
@@ -405,7 +406,8 @@ extern "C" void hd_flash_make_vt(const void *v, void *vt, int bh, int seq) {
 
 static int fa_launch(const void *q, const void *k, const void *vt, const void *mask, void *out,
                      int batch, int hq, int hkv, int seq, int ar_len, int q_row_end, float scale,
-                     int out_seq_major, hipStream_t st, void *ws = nullptr, int64_t ws_bytes = 0) {
+                     int out_seq_major, hipStream_t st, void *ws = nullptr, int64_t ws_bytes = 0,
+                     int out_rows = 0) {
     FaArgs a;
     a.q = (const uint16_t *)q;
     a.k = (const uint16_t *)k;
@@ -421,6 +423,7 @@ static int fa_launch(const void *q, const void *k, const void *vt, const void *m
     a.scale_log2 = scale * 1.44269504088896341f;
     a.inv_scale = 1.0f / scale;
     a.out_seq_major = out_seq_major;
+    a.out_rows = out_rows > 0 ? out_rows : seq;
     // 8-wave blocks (one copy of each K / V^T tile for 256 queries) when the
     // tail split can fill the last round and the sequence is long enough to
     // amortise the larger block: +3 % at S = 16640 / 16896, equal at 4352;
@@ -509,6 +512,7 @@ struct hd_sdpa_plan {
     size_t vt_bytes;
     void *ws = nullptr;      // tail-split partials (hd_flash_ws_bytes)
     int64_t ws_bytes = 0;
+    void *o_stage = nullptr; // split plans: causal-prefix rows of pass 0, [B, ar_len, Hq, D]
 };
 
 static int sdpa_err(const char *m) {
@@ -540,6 +544,13 @@ static int plan_new(hd_sdpa_plan **out, int batch, int hq, int hkv, int sq, int 
         delete p;
         return sdpa_err("hipMalloc flash workspace failed");
     }
+    if (ar_len > 0 &&
+        hipMalloc(&p->o_stage, (size_t)batch * ar_len * hq * d * 2) != hipSuccess) {
+        (void)hipFree(p->vt);
+        (void)hipFree(p->ws);
+        delete p;
+        return sdpa_err("hipMalloc causal-prefix staging failed");
+    }
     *out = p;
     return 0;
 }
@@ -569,16 +580,20 @@ extern "C" void hd_sdpa_destroy(hd_sdpa_plan *p) {
     if (!p) return;
     if (p->vt) (void)hipFree(p->vt);
     if (p->ws) (void)hipFree(p->ws);
+    if (p->o_stage) (void)hipFree(p->o_stage);
     delete p;
 }
 
 static int plan_run(hd_sdpa_plan *p, const void *q, const void *k, const void *v, const void *mask,
-                    void *out, void *stream, int ar_len, int q_row_end) {
+                    void *out, void *stream, int ar_len, int q_row_end, bool to_stage = false) {
     hipStream_t st = stream ? (hipStream_t)stream : hd_stream();
     dim3 g(hd_cdiv(fa_spad(p->Skv), 64), p->B * p->Hkv);
     fa_vt_kernel<<<g, 256, 0, st>>>((const uint16_t *)v, (uint16_t *)p->vt, p->Skv,
                                     (int)fa_spad(p->Skv));
     if (hipGetLastError() != hipSuccess) return sdpa_err("V^T staging launch failed");
+    if (to_stage)   // pass 0: the causal rows into the plan's staging, seq-major
+        return fa_launch(q, k, p->vt, mask, p->o_stage, p->B, p->Hq, p->Hkv, p->Sq, ar_len, q_row_end,
+                         p->scale, 1, st, p->ws, p->ws_bytes, p->ar_len);
     return fa_launch(q, k, p->vt, mask, out, p->B, p->Hq, p->Hkv, p->Sq, ar_len, q_row_end,
                      p->scale, 0, st, p->ws, p->ws_bytes);
 }
@@ -597,11 +612,16 @@ extern "C" int hd_sdpa_execute_split(hd_sdpa_plan *p, const void *q, const void 
     return plan_run(p, q, k, v, nullptr, out, stream, p->ar_len, p->Sq);
 }
 
+extern "C" const void *hd_sdpa_plan_stage(const hd_sdpa_plan *p) { return p ? p->o_stage : nullptr; }
+
 extern "C" int hd_sdpa_execute_split_pass(hd_sdpa_plan *p, int which, const void *q, const void *k,
                                           const void *v, void *out, void *stream) {
     if (!p || !q || !k || !v || !out) return sdpa_err("null arg in execute");
     if (p->ar_len <= 0) return sdpa_err("execute_split_pass on a non-split plan");
-    if (which == 0) return plan_run(p, q, k, v, nullptr, out, stream, p->ar_len, p->ar_len);
+    // pass 0 leaves `out` untouched: its rows go to the plan's staging, as
+    // the reference's causal pass writes only its staged head
+    // (hd_cudnn_sdpa.cu:455-468)
+    if (which == 0) return plan_run(p, q, k, v, nullptr, out, stream, p->ar_len, p->ar_len, true);
     return plan_run(p, q, k, v, nullptr, out, stream, 0, p->Sq);
 }
 

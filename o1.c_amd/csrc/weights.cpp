@@ -141,13 +141,20 @@ extern "C" hd_status hd_weights_to_device_gguf(const char *path, int device_id, 
     info.upload_stream = us;
     {
         Staging sg;
-        for (int k = 0; k < kSlots; k++)
-            if (hipHostMalloc(&sg.buf[k], kSlotBytes, hipHostMallocDefault) != hipSuccess ||
-                hipEventCreateWithFlags(&sg.ev[k], hipEventDisableTiming) != hipSuccess) {
+        for (int k = 0; k < kSlots; k++) {
+            // each allocation checked on its own: the Staging destructor
+            // frees whatever did succeed
+            if (hipHostMalloc(&sg.buf[k], kSlotBytes, hipHostMallocDefault) != hipSuccess) {
                 sg.buf[k] = nullptr;
                 werr("pinned staging allocation failed");
                 return fail(HD_ERR_OOM);
             }
+            if (hipEventCreateWithFlags(&sg.ev[k], hipEventDisableTiming) != hipSuccess) {
+                sg.ev[k] = nullptr;
+                werr("staging event creation failed");
+                return fail(HD_ERR_OOM);
+            }
+        }
         const int fd = open(path, O_RDONLY);
         if (fd < 0) {
             werr("open %s: %s", path, strerror(errno));

@@ -255,6 +255,7 @@ SIGNATURES = {
     "hd_sdpa_create_split": (c_int, [ctypes.POINTER(c_void_p), c_int, c_int, c_int, c_int, c_int, c_int, c_float]),
     "hd_sdpa_execute_split": (c_int, [P, P, P, P, P, P]),
     "hd_sdpa_execute_split_pass": (c_int, [P, c_int, P, P, P, P, P]),
+    "hd_sdpa_plan_stage": (P, [P]),
     "hd_sdpa_create_prod": (c_int, [ctypes.POINTER(c_void_p), c_int, c_int, c_int, c_int, c_int, c_int, c_float]),
     "hd_flash_attention": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int]),
     "hd_sdpa_plan_ar_len": (c_int, [P]),

@@ -308,6 +308,39 @@ def test_flash_tile_edges(pkg, lib, dev, Hq, Hkv, S, ar):
     assert rel_l2(got, ref) < 8e-3 and cosine(got, ref) > 0.99995
 
 
+def test_sdpa_split_passes(pkg, lib, dev):
+    """hd_sdpa_execute_split_pass: pass 0 writes the causal head rows into
+    the plan's staging and leaves `out` untouched (hd_cudnn_sdpa.cu:455-468),
+    pass 1 writes every row with full attention; the staged rows equal the
+    causal rows of hd_sdpa_execute_split bit for bit."""
+    Hq, Hkv, S, D, ar = 8, 2, 300, 128, 77
+    q, k, v = _attn_inputs(Hq, Hkv, S, D, 5)
+    plan = pkg.SdpaPlan(1, Hq, Hkv, S, D, ar_len=ar)
+    qd, kd, vd = dbf(q, dev), dbf(k, dev), dbf(v, dev)
+    full = torch.empty(Hq, S, D, dtype=torch.bfloat16, device=dev)
+    assert lib.hd_sdpa_execute_split(plan.h, pkg.ptr(qd), pkg.ptr(kd), pkg.ptr(vd), pkg.ptr(full), None) == 0
+    out = torch.full((Hq, S, D), 7.0, dtype=torch.bfloat16, device=dev)
+    assert lib.hd_sdpa_execute_split_pass(plan.h, 0, pkg.ptr(qd), pkg.ptr(kd), pkg.ptr(vd), pkg.ptr(out),
+                                          None) == 0
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())
+    stage_ptr = lib.hd_sdpa_plan_stage(plan.h)
+    assert stage_ptr
+    # read the staging through an exact kernel: bf16(x + 0) = x
+    stage = torch.empty(ar, Hq, D, dtype=torch.bfloat16, device=dev)
+    zeros = torch.zeros_like(stage)
+    lib.hd_residual_add(ctypes.c_void_p(stage_ptr), pkg.ptr(zeros), pkg.ptr(stage), stage.numel())
+    pkg.check_prim("stage read")
+    torch.cuda.synchronize()
+    assert torch.equal(stage.transpose(0, 1), full[:, :ar])
+    assert lib.hd_sdpa_execute_split_pass(plan.h, 1, pkg.ptr(qd), pkg.ptr(kd), pkg.ptr(vd), pkg.ptr(out),
+                                          None) == 0
+    torch.cuda.synchronize()
+    ref = orc.attention(q, k, v, None, 0, round_=0)
+    got = host(out).transpose(1, 0, 2).reshape(S, Hq * D)
+    assert rel_l2(got, ref) < 8e-3 and cosine(got, ref) > 0.99995
+
+
 @pytest.mark.parametrize("order", [1, 2])
 def test_unipc_kernels_match_oracle(pkg, lib, dev, order):
     # hd_unipc_* against the C restatement, bit for bit, including the last
