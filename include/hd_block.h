@@ -79,9 +79,10 @@ int64_t hd_decoder_block_scratch_bytes(int64_t seq, int heads, int kv_heads,
 hd_status hd_block_resolve(const hd_weight_store *wstore, int layer_idx,
                            hd_block_binding *out);
 
-/* block.h:88 - one block, batch 1. pos_dev fp32 [3,seq]; sec_dev is kept
- * for signature compatibility (the section is taken from the block config;
- * the device copy is not read). mask_dev: [seq,seq] bf16 additive mask,
+/* block.h:88 - one block, batch 1. pos_dev fp32 [3,seq]; sec_dev: the MRoPE
+ * section, int64[3] in device memory, read by the rotary-table kernel (NULL:
+ * the block config's section; theta, eps and interleaving always come from
+ * the block config, as the reference hard-codes them). mask_dev: [seq,seq] bf16 additive mask,
  * used when `sdpa` is NULL or is a non-split plan; may be NULL (no mask).
  * in_dev and out_dev must not overlap the scratch. out_dev may equal
  * in_dev (in-place update): the input is last read by the o_proj epilogue,

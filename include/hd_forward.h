@@ -99,7 +99,8 @@ int64_t hd_forward_workspace_bytes(int64_t seq, int img_tokens, int heads,
                                    int kv_heads, int hidden, int ff_hidden,
                                    int head_dim, int64_t *block_scratch_bytes);
 
-/* forward.h:156 */
+/* forward.h:156. sec_dev: the MRoPE section, int64[3] in device memory, read
+ * by the rotary-table kernel (NULL: the block config's section). */
 hd_status hd_forward(const hd_forward_binding *bw, hd_forward_workspace *ws,
                      const int64_t *input_ids, int text_len,
                      const float *pos_f32, const void *mask_dev,

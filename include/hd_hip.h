@@ -165,6 +165,11 @@ void hd_add_rmsnorm(const void *x_dev, const void *a_dev, const void *w_dev,
 void hd_rope_table(const float *pos_dev, int seq, const int64_t *section_host,
                    int n_section, int head_dim, float theta,
                    float attention_scaling, int interleaved, float *cs_dev);
+/* The same table with the section in device memory (int64[n_section], as
+ * the reference's sec_dev), read by the kernel. */
+void hd_rope_table_dev(const float *pos_dev, int seq, const int64_t *section_dev,
+                       int n_section, int head_dim, float theta,
+                       float attention_scaling, int interleaved, float *cs_dev);
 
 /* QKV epilogue: qkv [B*S, (H+2KV)*D] projection output ->
  *   q  [B,H,S,D]  = rope(rmsnorm_D(q_proj) * q_norm)

@@ -192,7 +192,6 @@ extern "C" hd_status hd_decoder_block(const void *in_dev, const float *pos_dev,
                                       void *out_dev, int64_t seq, int heads, int kv_heads,
                                       int hidden, int ff_hidden, int head_dim,
                                       hd_sdpa_plan *sdpa) {
-    (void)sec_dev;
     if (!in_dev || !pos_dev || !binding_ok(bw) || !scratch || !out_dev) {
         hd_set_error("block: null argument");
         return HD_ERR_MISSING;
@@ -209,8 +208,14 @@ extern "C" hd_status hd_decoder_block(const void *in_dev, const float *pos_dev,
     }
     BlockScratch s = carve(scratch, 1, seq, heads, kv_heads, hidden, ff_hidden, head_dim, true);
     hd_cuda_clear_error();
-    hd_rope_table(pos_dev, (int)seq, g_cfg.section, 3, head_dim, g_cfg.rope_theta,
-                  g_cfg.attention_scaling, g_cfg.interleaved, s.cs);
+    // the caller's device section when given (block.c:233-236 passes it to
+    // hd_mrope_cos_sin), else the block config's
+    if (sec_dev)
+        hd_rope_table_dev(pos_dev, (int)seq, sec_dev, 3, head_dim, g_cfg.rope_theta,
+                          g_cfg.attention_scaling, g_cfg.interleaved, s.cs);
+    else
+        hd_rope_table(pos_dev, (int)seq, g_cfg.section, 3, head_dim, g_cfg.rope_theta,
+                      g_cfg.attention_scaling, g_cfg.interleaved, s.cs);
     // Split plans reproduce the causal text prefix structurally and ignore
     // the dense mask (hd_cudnn_sdpa.cu:269-272); otherwise the mask is the
     // additive bias, as in the eager path.

@@ -320,6 +320,36 @@ extern "C" void hd_rope_table(const float *pos_dev, int seq, const int64_t *sect
     hd_check_launch("rope_table");
 }
 
+// The same table with the section read from device memory (the reference's
+// int64[3] sec_dev, rope.cu:73-95), so a caller's per-call section is honoured
+// without a host round trip.
+__global__ void rope_table_dev_kernel(const float *pos, const int64_t *sec_dev, float2 *cs, int seq,
+                                      int dim, float theta, float scaling, int n_section,
+                                      int interleaved) {
+    int half = dim / 2;
+    int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= seq * half) return;
+    int64_t sec[3] = {0, 0, 0};
+    for (int i = 0; i < n_section; i++) sec[i] = sec_dev[i];
+    int s = idx / half, f = idx % half;
+    int row = rope_row(f, sec, n_section, interleaved);
+    float p = pos[(size_t)row * seq + s];
+    float base = expf(-logf(theta) * (2.0f * (float)f) / (float)dim);
+    float ang = base * p;
+    cs[idx] = make_float2(cosf(ang) * scaling, sinf(ang) * scaling);
+}
+extern "C" void hd_rope_table_dev(const float *pos_dev, int seq, const int64_t *section_dev,
+                                  int n_section, int head_dim, float theta, float attention_scaling,
+                                  int interleaved, float *cs_dev) {
+    if (!pos_dev || !section_dev || !cs_dev || seq <= 0 || head_dim <= 0 || head_dim % 2 ||
+        n_section < 1 || n_section > 3)
+        BAD("rope_table_dev");
+    rope_table_dev_kernel<<<hd_cdiv((size_t)seq * head_dim / 2, 256), 256, 0, hd_stream()>>>(
+        pos_dev, section_dev, (float2 *)cs_dev, seq, head_dim, theta, attention_scaling, n_section,
+        interleaved);
+    hd_check_launch("rope_table_dev");
+}
+
 static bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 // Rotate-half rotation on [heads, seq, dim] (rope.cu:97-134 / :157-180).

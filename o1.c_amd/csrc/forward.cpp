@@ -164,7 +164,8 @@ static hd_status forward_core(const hd_forward_binding *bw, hd_forward_workspace
                               int ar_len, const void *vin, int I, const float *tstep, int S,
                               int H, int KV, int HID, int FF, int D, int tms,
                               hd_forward_diagnostics *dg, void *out,
-                              const hd_visual_cond *vis = nullptr) {
+                              const hd_visual_cond *vis = nullptr,
+                              const int64_t *sec_dev = nullptr) {
     const hd_block_config *cfg;
     hd_block_config c;
     hd_block_get_config(&c);
@@ -231,8 +232,12 @@ static hd_status forward_core(const hd_forward_binding *bw, hd_forward_workspace
         if ((s = d2d(dg->after_block_0_input, hidden, (size_t)S * row, st)) != HD_OK) return s;
     }
 
-    hd_rope_table(pos, S, cfg->section, 3, D, cfg->rope_theta, cfg->attention_scaling,
-                  cfg->interleaved, cs);
+    if (sec_dev)   // the caller's device section (forward.c passes sec_dev to every block)
+        hd_rope_table_dev(pos, S, sec_dev, 3, D, cfg->rope_theta, cfg->attention_scaling,
+                          cfg->interleaved, cs);
+    else
+        hd_rope_table(pos, S, cfg->section, 3, D, cfg->rope_theta, cfg->attention_scaling,
+                      cfg->interleaved, cs);
     if ((s = fwd_err("rope table")) != HD_OK) return s;
 
     const int n = bw->n_layers;
@@ -295,7 +300,6 @@ extern "C" hd_status hd_forward(const hd_forward_binding *bw, hd_forward_workspa
                                 const int64_t *sec_dev, int seq, int heads, int kv_heads,
                                 int hidden, int ff_hidden, int head_dim, int tms_token_id,
                                 hd_forward_diagnostics *diag, void *out_dev, void *stream) {
-    (void)sec_dev;
     if (!bw || !ws || (!input_ids && text_len > 0) || !pos_f32 || !vinputs || !timestep || !out_dev) {
         hd_set_error("forward: null argument");
         return HD_ERR_MISSING;
@@ -312,7 +316,7 @@ extern "C" hd_status hd_forward(const hd_forward_binding *bw, hd_forward_workspa
     const void *mask = ar_len > 0 ? nullptr : mask_dev;
     return forward_core(bw, ws, 1, input_ids, text_len, pos_f32, mask, ar_len, vinputs, img_tokens,
                         timestep, seq, heads, kv_heads, hidden, ff_hidden, head_dim, tms_token_id,
-                        diag, out_dev, visual);
+                        diag, out_dev, visual, sec_dev);
 }
 
 extern "C" hd_status hd_forward_batched(const hd_forward_binding *bw, hd_forward_workspace *ws,

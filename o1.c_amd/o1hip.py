@@ -217,6 +217,7 @@ SIGNATURES = {
     "hd_sched_cfg_guided": (None, [P, P, c_float, P, c_int]),
     "hd_add_rmsnorm": (None, [P, P, P, P, P, c_int, c_int, c_float]),
     "hd_rope_table": (None, [P, c_int, P, c_int, c_int, c_float, c_float, c_int, P]),
+    "hd_rope_table_dev": (None, [P, c_int, P, c_int, c_int, c_float, c_float, c_int, P]),
     "hd_qkv_epilogue": (None, [P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float]),
     "hd_transpose_sd": (None, [P, P, c_int, c_int, c_int]),
     "hd_patchify_f32": (None, [P, P, c_int, c_int, c_int, c_int]),

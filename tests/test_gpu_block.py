@@ -177,3 +177,44 @@ def test_block_config1_full_size(pkg, lib, dev):
         check(got[rows], ref[rows], x.numpy()[rows], f"config1 seq {b} vs fp32")
     reff = oracle_block(w, x.numpy(), pos, H, KV, HID, FF, D, 1e4, faithful=1, batch=B)
     check(got, reff, x.numpy(), "config1 vs bf16-faithful", rel=5e-3, cos=0.99995, delta=3e-2)
+
+
+def test_block_reads_device_section(pkg, lib, dev):
+    """sec_dev (int64[3] on the device, block.c:233-236) selects the MRoPE
+    section: a non-default section through sec_dev equals the same section
+    set through the block config bit for bit, and the oracle with that
+    section within the bound."""
+    H, KV, HID, FF, D = 4, 2, 512, 1024, 128
+    T, gh, gw = 16, 8, 12
+    S = T + gh * gw
+    sec = (16, 24, 24)
+    w = make_block_weights(HID, H, KV, FF, D, seed=21)
+    x = bf16(torch.randn(S, HID, generator=torch.Generator().manual_seed(22)))
+    pos = grid_pos(T, gh, gw)
+    pos[0, T:] = 2000.0                 # a T axis far from H: the section rule matters
+    pkg.set_block_config(theta=1e4)
+    wd = {k: to_dev(v, dev) for k, v in w.items()}
+    bind = pkg.binding_from(wd)
+    xd = x.to(dev, torch.bfloat16)
+    posd = torch.from_numpy(pos).to(dev)
+    secd = torch.tensor(sec, dtype=torch.int64, device=dev)
+    nbytes = lib.hd_decoder_block_scratch_bytes(S, H, KV, HID, FF, D)
+    scratch = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    outs = []
+    for use_dev in (True, False):
+        if not use_dev:
+            pkg.set_block_config(theta=1e4, section=sec)
+        out = torch.empty_like(xd)
+        st = lib.hd_decoder_block(pkg.ptr(xd), pkg.ptr(posd), None, bind, pkg.ptr(secd) if use_dev else None,
+                                  pkg.ptr(scratch), nbytes, None, pkg.ptr(out), S, H, KV, HID, FF, D, None)
+        pkg.check_status(st, "hd_decoder_block sec_dev")
+        torch.cuda.synchronize()
+        outs.append(out.clone())
+    assert torch.equal(outs[0], outs[1])
+    cfg = orc.block_cfg(H, KV, HID, FF, D, theta=1e4, faithful=0, section=sec)
+    ref = orc.decoder_block(x.numpy(), pos, {k: v.numpy() for k, v in w.items()}, cfg)
+    check(outs[0].float().cpu().numpy(), ref, x.numpy(), "sec_dev block vs fp32")
+    cfg_def = orc.block_cfg(H, KV, HID, FF, D, theta=1e4, faithful=0)
+    ref_def = orc.decoder_block(x.numpy(), pos, {k: v.numpy() for k, v in w.items()}, cfg_def)
+    xn = x.numpy()
+    assert rel_l2(ref - xn, ref_def - xn) > 1e-2    # the section changes the block's update
