@@ -136,9 +136,10 @@ int hd_linear_qkv_rope_ws(const void *x, const void *wq, const void *wk, const v
 
 /* Diagnostics/tuning: kernel family for the production GEMMs. 0 (default):
  * 8-wave fragment-ring tiles with buffer loads for every K (the fused QKV
- * epilogue included); 1: the previous kernels, 4-wave fragment-ring tiles
- * for K <= 8192 and 8-wave interleaved tiles above. Both compute identical
- * values. Returns the previous value. */
+ * epilogue included), the A operand's LDS ring three stages deep and B's
+ * two; 2: the same tiles with both rings two stages deep; 1: the previous
+ * kernels, 4-wave fragment-ring tiles for K <= 8192 and 8-wave interleaved
+ * tiles above. All compute identical values. Returns the previous value. */
 int hd_gemm_set_family(int family);
 
 #ifdef __cplusplus

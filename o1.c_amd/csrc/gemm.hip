@@ -314,7 +314,7 @@ template <int N> __device__ __forceinline__ void wait_lgk_vm_barrier() {
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int MF = 32>
+template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int MF = 32, int XA = 0, int XB = 0>
 struct MsCfg {
     static constexpr int NW = WGM * WGN, NT = NW * 64;
     static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / MF, TN = WTN / MF;
@@ -326,7 +326,8 @@ struct MsCfg {
     static constexpr int LPT = AI + BI;           // per tile per wave
     static constexpr int STAGE = (BM + BN) * BK;  // elements per stage
     static constexpr int EPAD = 8;
-    static constexpr int MAIN_BYTES = NS * STAGE * 2;
+    // XA / XB extra A / B stages (schedules 4, 5): rings NS + XA and NS + XB deep
+    static constexpr int MAIN_BYTES = ((NS + XA) * BM + (NS + XB) * BN) * BK * 2;
     static constexpr int EPI_BYTES = NW * WTM * (WTN_OUT + EPAD) * 2;
     static constexpr int LDS_BYTES = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
     static_assert(BK == 32 || BK == 64, "BK");
@@ -462,7 +463,9 @@ template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 0
 __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g) {
     // MF: MFMA shape, 32 (v_mfma_f32_32x32x16_bf16) or 16 (16x16x32, SGB 3 only)
     static_assert(MF == 32 || SGB == 3, "16x16 MFMA tiles use the continuous ring");
-    using C = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI, MF>;
+    static_assert((SGB != 4 && SGB != 5) || (LDR == 5 && MF == 32 && NS == 2),
+                  "split rings: buffer loads, 2+1 stages");
+    using C = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI, MF, SGB == 4 ? 1 : 0, SGB == 5 ? 1 : 0>;
     using AccT = typename std::conditional<MF == 32, f32x16_t, f32x4_t>::type;
     constexpr int ACCN = MF == 32 ? 16 : 4;
     constexpr int WTM = C::WTM, WTN = C::WTN, TM = C::TM, TN = C::TN, CPR = C::CPR;
@@ -693,6 +696,115 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
         for (; kt + NS < nk; kt++) tile(kt, T_{}, T_{});
         for (; kt + 1 < nk; kt++) tile(kt, F_{}, T_{});
         tile(kt, F_{}, F_{});
+    } else if constexpr (SGB == 4 || SGB == 5) {
+        // The fragment ring of schedule 3 with split operand rings in the
+        // 160 KB of LDS: one operand three stages deep, the other two
+        // (schedule 4: A deep - the activation rows, shared by fewer of an
+        // XCD's concurrent tiles, so more of their slices miss L2; schedule
+        // 5: B deep). Each refill batch issues the shallow operand's tile
+        // kt+2 before the deep operand's tile kt+3, so the wait at the end of
+        // tile kt (both operands of tile kt+1 landed) may leave the newest
+        // deep loads in flight: the deep operand gets two tiles of latency,
+        // the other one.
+        constexpr bool DA = SGB == 4;
+        constexpr int KS = BK / 16, NR = TM + TN, NM = TM * TN, AI_ = C::AI, BI_ = C::BI;
+        constexpr int NSA = NS + (DA ? 1 : 0), NSB = NS + (DA ? 0 : 1), ASTG = BM * BK, BSTG = BN * BK;
+        constexpr int ND = DA ? AI_ : BI_, NSH = DA ? BI_ : AI_;   // loads per batch: deep, shallow
+        static_assert(KS % 2 == 0, "fragment slots");
+        uint16_t *const Abase = smem, *const Bbase = smem + NSA * ASTG;
+        const int lr = lane % 32, lc = lane / 32, swr = ms_swz<CPR>(lr);
+        bf16x8_t af[2][TM], bw[2][TN];
+        auto ld = [&](int kt, int ks, int sl) {
+            const uint16_t *As = Abase + (kt % NSA) * ASTG, *Bs = Bbase + (kt % NSB) * BSTG;
+            const int c = ((ks * 2 + lc) ^ swr) * 8;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                af[sl][i] = *(const bf16x8_t *)(As + (wm * WTM + i * 32 + lr) * BK + c);
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                bw[sl][j] = *(const bf16x8_t *)(Bs + (wn * WTN + j * 32 + lr) * BK + c);
+        };
+        auto issue_a = [&](int kt) {
+            uint16_t *As = Abase + (kt % NSA) * ASTG;
+            const uint32_t so = (uint32_t)(kbase + kt) * BK * 2;
+#pragma unroll
+            for (int i = 0; i < AI_; i++)
+                buf_load_lds16(bp_a, nb_a, a_vo[i], so, (HD_LDS void *)(As + (wave * AI_ + i) * 512));
+        };
+        auto issue_b = [&](int kt) {
+            uint16_t *Bs = Bbase + (kt % NSB) * BSTG;
+            const uint32_t so = (uint32_t)(kbase + kt) * BK * 2;
+#pragma unroll
+            for (int i = 0; i < BI_; i++)
+                buf_load_lds16(b_rs[i] ? bp_b1 : bp_b0, nb_b, b_vo[i], so,
+                               (HD_LDS void *)(Bs + (wave * BI_ + i) * 512));
+        };
+        auto issue_deep = [&](int kt) {
+            if constexpr (DA) issue_a(kt);
+            else issue_b(kt);
+        };
+        auto issue_shallow = [&](int kt) {
+            if constexpr (DA) issue_b(kt);
+            else issue_a(kt);
+        };
+        // prologue: [S0 D0] [S1 D1] [D2]; tile 0 may leave the later ones in flight
+        issue_shallow(0);
+        issue_deep(0);
+        if (nk >= 2) {
+            issue_shallow(1);
+            issue_deep(1);
+        }
+        if (nk >= 3) {
+            issue_deep(2);
+            wait_vm_barrier<NSH + 2 * ND>();
+        } else if (nk == 2) {
+            wait_vm_barrier<NSH + ND>();
+        } else {
+            wait_vm_barrier<0>();
+        }
+        ld(0, 0, 0);
+        // RD: deep tile kt+3 exists, RS: shallow tile kt+2 exists, NX: tile kt+1 exists
+        auto tile = [&](int kt, auto rd, auto rs, auto nx) {
+            constexpr bool RD = decltype(rd)::value, RS = decltype(rs)::value, NX = decltype(nx)::value;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                const bool last = ks + 1 == KS;
+                if (!last) {
+                    ld(kt, ks + 1, (ks + 1) & 1);
+                } else {
+                    // both operands of tile kt+1 have landed (the deep
+                    // operand's tile kt+2, issued after them, may still fly)
+                    // and every wave is done reading the stages of tile kt
+                    if (RS) wait_lgk_vm_barrier<ND>();
+                    else wait_lgk_vm_barrier<0>();
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (RS) issue_shallow(kt + 2);
+                    if (RD) issue_deep(kt + 3);
+                    if (NX) ld(kt + 1, 0, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[ks & 1][j], af[ks & 1][i],
+                                                                             acc[i][j], 0, 0, 0);
+                const int nv = last ? (RD ? ND : 0) + (RS ? NSH : 0) : 0;
+                const int nr = !last || NX ? NR : 0;
+#pragma unroll
+                for (int q = 0; q < NM; q++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    if (q < nv) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                    if (q < nr) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+            }
+        };
+        using T_ = std::true_type;
+        using F_ = std::false_type;
+        int kt = 0;
+        for (; kt + 3 < nk; kt++) tile(kt, T_{}, T_{}, T_{});
+        if (kt + 2 < nk) tile(kt++, F_{}, T_{}, T_{});
+        if (kt + 1 < nk) tile(kt++, F_{}, F_{}, T_{});
+        tile(kt, F_{}, F_{}, F_{});
     } else {
     if (LDR == 1) {
         // 2-stage ring through registers: load k+1 early, store it after the
@@ -1330,6 +1442,8 @@ static bool run_table(int cfg, GemmArgs &g) {
     case 50: launch_ms<256, 256, 64, 2, 2, 4, EPI, 3, 1, 5>(g); return true;  // 8-wave ring, buffer loads
     case 51: launch_ms<192, 256, 64, 2, 2, 4, EPI, 3, 1, 5>(g); return true;
     case 55: launch_ms<256, 256, 64, 2, 2, 4, EPI, 3, 1, 6>(g); return true;  // diag: no epilogue
+    case 56: launch_ms<256, 256, 64, 2, 2, 4, EPI, 4, 1, 5>(g); return true;  // split rings (A 3, B 2)
+    case 57: launch_ms<256, 256, 64, 2, 2, 4, EPI, 5, 1, 5>(g); return true;  // split rings (A 2, B 3)
     case 7: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 1>(g); return true;    // diag: compute only
     case 8: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 2>(g); return true;    // diag: loads only
     default: return false;
@@ -1344,7 +1458,7 @@ static int g_family = 0;   // hd_gemm_set_family
 
 extern "C" int hd_gemm_set_family(int family) {
     const int prev = g_family;
-    g_family = family == 1 ? 1 : 0;
+    g_family = family == 1 || family == 2 ? family : 0;
     return prev;
 }
 
@@ -1395,25 +1509,35 @@ static const char *pick_and_launch(GemmArgs &g, bool launch, void *ws = nullptr,
     }
     // Family 0 (production): 8 waves (2 x 4) of 128x64 with one fragment
     // ring across the K loop and buffer loads straight to LDS (each operand
-    // under 2 GiB: 32-bit byte offsets); two waves per SIMD cover each
-    // other's barrier and load-issue stalls. Family 1 (the previous
+    // under 2 GiB: 32-bit byte offsets), the A operand's LDS ring one stage
+    // deeper than B's (schedule 4); two waves per SIMD cover each other's
+    // barrier and load-issue stalls. Family 1 (the previous
     // kernels, kept for same-process comparisons): 4 waves of 128x128 for
     // K <= 8192, 8 interleaved waves for deeper K.
     const bool fits = (size_t)(g.M + 256) * g.K * 2 < ((size_t)1 << 31) &&
                       (size_t)g.N * g.K * 2 < ((size_t)1 << 31);
     const bool use192 = c192 < c256;
     const bool split256 = p256 > 1;
-    if (g_family == 0) {
+    if (g_family == 2 && fits) {
+        // the production family with equal-depth operand rings (schedule 3)
+        if (use192) {
+            if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 3, 1, 5>(g, ws, ws_bytes);
+            return "bf16_192x256x64_w2x4_ring_buf_s3";
+        }
+        if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 3, 1, 5>(g, ws, ws_bytes);
+        return "bf16_256x256x64_w2x4_ring_buf_s3";
+    }
+    if (g_family != 1) {
         if (use192) {
             if (fits) {
-                if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 3, 1, 5>(g, ws, ws_bytes);
+                if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 4, 1, 5>(g, ws, ws_bytes);
                 return "bf16_192x256x64_w2x4_ring_buf";
             }
             if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 3>(g, ws, ws_bytes);
             return "bf16_192x256x64_w2x4_ring";
         }
         if (fits) {
-            if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 3, 1, 5>(g, ws, ws_bytes);
+            if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 4, 1, 5>(g, ws, ws_bytes);
             return split256 ? "bf16_256x256x64_w2x4_ring_buf_tailsplit" : "bf16_256x256x64_w2x4_ring_buf";
         }
         if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 3>(g, ws, ws_bytes);
@@ -1497,9 +1621,15 @@ extern "C" int hd_linear_qkv_rope_ws(const void *x, const void *wq, const void *
     const bool split256 =
         ws && tail_split_of(t256, hidden / 64, (size_t)256 * 256 * 4, ws_bytes, (size_t)256 * 256 * 2) > 1;
     const bool use192 = !split256 && quant_eff(t192) > quant_eff(t256) * 1.12;
-    if (g_family == 0) {   // 8 waves: two 64-wide wave tiles per head
-        if (use192) launch_ms<192, 256, 64, 2, 2, 4, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
-        else launch_ms<256, 256, 64, 2, 2, 4, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
+    if (g_family != 1) {   // 8 waves: two 64-wide wave tiles per head
+        if (g_family == 2) {
+            if (use192) launch_ms<192, 256, 64, 2, 2, 4, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
+            else launch_ms<256, 256, 64, 2, 2, 4, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
+        } else if (use192) {
+            launch_ms<192, 256, 64, 2, 2, 4, EPI_QKV, 4, 1, 5>(g, ws, ws ? ws_bytes : 0);
+        } else {
+            launch_ms<256, 256, 64, 2, 2, 4, EPI_QKV, 4, 1, 5>(g, ws, ws ? ws_bytes : 0);
+        }
     } else {
         if (use192) launch_ms<192, 256, 64, 2, 2, 2, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
         else launch_ms<256, 256, 64, 2, 2, 2, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
