@@ -33,11 +33,16 @@ I = GH * GW
 STEPS = 3
 
 
-def oracle_loop(fw, cfg, seqs, z0, sig, guidance, sampler, seed=0, clip=0.0, sn=(1.0, 1.0)):
-    """seqs: [(ids, pos, T)] - one (conditional) or two (+ unconditional)."""
+def oracle_loop(fw, cfg, seqs, z0, sig, guidance, sampler, seed=0, clip=0.0, sn=(1.0, 1.0), unipc=None):
+    """seqs: [(ids, pos, T)] - one (conditional) or two (+ unconditional).
+    unipc: (lib, pkg, sched) for sampler 2 - the per-step plan comes from
+    hd_scheduler_unipc_plan (host code pinned bit-exact against the
+    reference's scheduler.c by the CPU tests)."""
     z = z0.copy()
     gen = torch.Generator().manual_seed(seed + 1)
     n = z.size
+    this_order = lower = have = 0
+    last = slot1 = slot2 = None
     for i in range(STEPS):
         s_i = np.float32(sig[i])
         sg = max(float(s_i), 1e-6)
@@ -49,6 +54,25 @@ def oracle_loop(fw, cfg, seqs, z0, sig, guidance, sampler, seed=0, clip=0.0, sn=
         mo = orc.sched_cfg_guided(mos[0], mos[1], guidance) if len(mos) == 2 else mos[0]
         if sampler == 0:
             z = orc.sched_flow_match_step(z, mo, sig[i], sig[i + 1])
+        elif sampler == 2:
+            # generate.c:1360-1410: convert, correct (from step 1 on, with
+            # history), predict, z = bf16(prediction), rotate the history
+            lib, pkg, sch = unipc
+            pl = pkg.hd_unipc_plan()
+            lib.hd_scheduler_unipc_plan(ctypes.byref(sch), i, this_order, lower, ctypes.byref(pl))
+            conv = orc.unipc_convert(z, mo, float(s_i))
+            corr = z
+            if i > 0 and this_order > 0 and have:
+                corr = orc.unipc_correct(last, slot1, slot2, conv, pl.c_sig_t, pl.c_sig_s0, pl.c_alpha_t,
+                                         pl.c_h_phi_1, pl.c_B_h, pl.c_rhos0, pl.c_rhos1, pl.c_inv_rks0,
+                                         pl.corr_order)
+            last = corr.copy()
+            pred = orc.unipc_predict(corr, conv, slot1 if slot1 is not None else conv, pl.p_sig_t,
+                                     pl.p_sig_s0, pl.p_alpha_t, pl.p_h_phi_1, pl.p_B_h, pl.p_rhos_p,
+                                     pl.p_inv_rks0, pl.pred_order)
+            z = bf16(torch.from_numpy(pred)).numpy()
+            slot2, slot1 = slot1, conv
+            this_order, lower, have = pl.next_this_order, pl.next_lower_order, 1
         else:
             noise = torch.randn(n, generator=gen).numpy().astype(np.float64)
             if clip > 0:
@@ -101,16 +125,20 @@ def ids_for(T, seed):
     return ids
 
 
-@pytest.mark.parametrize("sampler", [0, 1])
+@pytest.mark.parametrize("sampler", [0, 1, 2])
 def test_denoise_cfg_equal_length_vs_oracle_loop(pkg, lib, dev, sampler):
-    """hd_denoise, batch 2: cond and uncond ids of one length."""
+    """hd_denoise, batch 2: cond and uncond ids of one length (Euler, flash
+    SDE, FlowUniPC over the default schedule)."""
     keep, fb, ofw, cfg = setup(pkg, lib, dev)
     T = 16
     S = T + I
     ids = np.stack([ids_for(T, 1), ids_for(T, 2)])
     pos = grid_pos(T, GH, GW)
     sch = pkg.hd_scheduler()
-    lib.hd_scheduler_derive_flash(ctypes.byref(sch), STEPS, 3.0, 8.0)
+    if sampler == 2:
+        lib.hd_scheduler_derive_default(ctypes.byref(sch), STEPS, 3.0, 8.0)
+    else:
+        lib.hd_scheduler_derive_flash(ctypes.byref(sch), STEPS, 3.0, 8.0)
     sig = [sch.sigmas[i] for i in range(sch.num_steps)]
     z0 = bf16(torch.randn(I, 3072, generator=torch.Generator().manual_seed(5))).numpy()
     g, seed, clip, sn = 5.0, 77, 2.0, (1.0, 0.5)
@@ -126,8 +154,9 @@ def test_denoise_cfg_equal_length_vs_oracle_loop(pkg, lib, dev, sampler):
     torch.cuda.synchronize()
     z = zd.float().cpu().numpy()
     sq = [(ids[0], pos, T), (ids[1], pos, T)]
-    zo = oracle_loop(ofw, cfg[0], sq, z0, sig, g, sampler, seed, clip, sn)
-    zo32 = oracle_loop(ofw, cfg[1], sq, z0, sig, g, sampler, seed, clip, sn)
+    up = (lib, pkg, sch)
+    zo = oracle_loop(ofw, cfg[0], sq, z0, sig, g, sampler, seed, clip, sn, unipc=up)
+    zo32 = oracle_loop(ofw, cfg[1], sq, z0, sig, g, sampler, seed, clip, sn, unipc=up)
     compare(z, z0, zo, zo32, f"hd_denoise sampler {sampler}")
     lib.hd_forward_binding_free(ctypes.byref(fb))
 
