@@ -322,22 +322,27 @@ __global__ __launch_bounds__(256) void fa_vt_kernel(const uint16_t *v, uint16_t 
 }
 
 // Merges the tail units' key-chunk partials: O = sum_i w_i O_i / sum_i w_i l_i
-// with w_i = 2^((m_i - max_j m_j) * scale_log2). One thread per (row, d).
+// with w_i = 2^((m_i - max_j m_j) * scale_log2). One thread per (row, 8
+// consecutive d): two 16-byte partial loads per chunk, one 16-byte store.
 template <int BQ>
 __global__ __launch_bounds__(256) void fa_merge_kernel(FaArgs a, int n_tail) {
     const int idx = blockIdx.x * 256 + threadIdx.x;
-    const int d = idx % FA_D, row = (idx / FA_D) % BQ, tu = idx / (FA_D * BQ);
+    const int d0 = (idx % (FA_D / 8)) * 8, row = (idx / (FA_D / 8)) % BQ, tu = idx / (FA_D / 8 * BQ);
     if (tu >= n_tail) return;
     const int P = a.split, n_items = n_tail * P;
     const float2 *pml = (const float2 *)(a.part + (size_t)n_items * BQ * FA_D);
     float m = -INFINITY;
     for (int i = 0; i < P; i++) m = fmaxf(m, pml[(size_t)(tu * P + i) * BQ + row].x);
-    float L = 0.f, acc = 0.f;
+    float L = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int i = 0; i < P; i++) {
         const float2 ml = pml[(size_t)(tu * P + i) * BQ + row];
         const float w = __builtin_amdgcn_exp2f((ml.x - m) * a.scale_log2);
         L = fmaf(w, ml.y, L);
-        acc = fmaf(w, a.part[((size_t)(tu * P + i) * BQ + row) * FA_D + d], acc);
+        const float4 *src = (const float4 *)(a.part + ((size_t)(tu * P + i) * BQ + row) * FA_D + d0);
+        const float4 p0 = src[0], p1 = src[1];
+        const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[e] = fmaf(w, pv[e], acc[e]);
     }
     const int nqt = (a.q_row_end + BQ - 1) / BQ, group = a.Hq / a.Hkv;
     int lin = a.n_whole + tu;
@@ -346,9 +351,13 @@ __global__ __launch_bounds__(256) void fa_merge_kernel(FaArgs a, int n_tail) {
     const int hk = lin % a.Hkv, b = lin / a.Hkv, hq = hk * group + g;
     const int my_q = qt * BQ + row;
     if (my_q >= a.q_row_end) return;
-    const size_t o = a.out_seq_major ? (((size_t)b * a.out_rows + my_q) * a.Hq + hq) * FA_D + d
-                                     : (((size_t)b * a.Hq + hq) * a.out_rows + my_q) * FA_D + d;
-    a.out[o] = f2bf(acc * (1.0f / L));
+    const size_t o = a.out_seq_major ? (((size_t)b * a.out_rows + my_q) * a.Hq + hq) * FA_D + d0
+                                     : (((size_t)b * a.Hq + hq) * a.out_rows + my_q) * FA_D + d0;
+    const float inv = 1.0f / L;
+    u32x4_t v;
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = pack_bf2(acc[2 * e] * inv, acc[2 * e + 1] * inv);
+    *(u32x4_t *)(a.out + o) = v;
 }
 
 // Resident flash blocks on the current device (occupancy x CUs), cached.
@@ -462,7 +471,7 @@ static int fa_launch(const void *q, const void *k, const void *vt, const void *m
         else flash_fwd_kernel<false, 4><<<grid, 256, 0, st>>>(a);
     }
     if (n_tail) {
-        dim3 gm((unsigned)hd_cdiv((int64_t)n_tail * BQ * FA_D, 256));
+        dim3 gm((unsigned)hd_cdiv((int64_t)n_tail * BQ * (FA_D / 8), 256));
         if (nwv == 8) fa_merge_kernel<256><<<gm, 256, 0, st>>>(a, n_tail);
         else fa_merge_kernel<128><<<gm, 256, 0, st>>>(a, n_tail);
     }
