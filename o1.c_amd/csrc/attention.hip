@@ -85,6 +85,15 @@ __device__ __forceinline__ float xor32_sum(float v) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Blocks are dispatched to the 8 XCDs round-robin (block b to XCD b % 8):
+// give each XCD a contiguous range of linear ids instead, so the blocks one
+// XCD runs at a time share their kv heads' K / V^T in that XCD's L2.
+__device__ __forceinline__ int fa_xcd_remap(int b, int nb) {
+    const int per = nb / 8, rem = nb % 8;
+    const int xcd = b % 8, idx = b / 8;
+    return xcd * per + (xcd < rem ? xcd : rem) + idx;
+}
+
 // NWV waves per block (4: two blocks per CU; 8: one block of 256 queries
 // per CU sharing one copy of the K / V^T tiles); 32 queries per wave either way.
 template <bool MASKED, int NWV>
@@ -104,6 +113,8 @@ __global__ __launch_bounds__(NWV * 64, 8 / NWV) void flash_fwd_kernel(FaArgs a) 
         item = lin - a.n_whole;
         chunk = item % a.split;
         lin = a.n_whole + item / a.split;
+    } else {
+        lin = fa_xcd_remap(lin, a.n_whole);
     }
     const int g = lin % group; lin /= group;
     const int qt = lin % nqt; lin /= nqt;
