@@ -538,7 +538,10 @@ def run_c4(pkg, lib, model, tensors, cfg, ws, ids, posd, vin, T, I, S, dev, args
     assert torch.isfinite(zf).all(), "non-finite latent"
     lora = {"targets": k, "rank": r, "merge_ms": round(merge_ms, 3), "weight_elems": welems,
             "hbm_gb_s": round(welems * 4 / (merge_ms * 1e-3) / 1e9, 1),
-            "fp32_tflops": round(welems * 2 * r / (merge_ms * 1e-3) / 1e12, 2)}
+            "hbm_frac": round(welems * 4 / (merge_ms * 1e-3) / 8e12, 4),
+            "fp32_tflops": round(welems * 2 * r / (merge_ms * 1e-3) / 1e12, 2),
+            "fp32_matrix_frac": round(welems * 2 * r / (merge_ms * 1e-3) / 157.3e12, 4),
+            "kernel": "lora_merge_stream_kernel (rank product on bf16 MFMA, fp32 operands split in 3 bf16 parts)"}
     if not args.no_cpu_baseline:
         lora["cpu_baseline"] = cpu_lora_baseline(r, welems)
     return {"lora": lora,

@@ -1,9 +1,13 @@
 // GPU LoRA merge-on-load: W = bf16(float(W) + s * (up @ down)), fp32 delta.
-// Replaces hd_lora_merge_gpu (lora_merge.cu:35-104). One kernel per target:
-// a block owns a tile of W, stages the matching slice of `up` and of `down`
-// in LDS (r in chunks of 64), forms the fp32 delta in registers and does the
-// single read-modify-write of W. The delta never reaches HBM; nothing is
-// allocated.
+// Replaces hd_lora_merge_gpu (lora_merge.cu:35-104). One launch per target;
+// the delta never reaches HBM and nothing is allocated. Three kernels:
+//  - lora_merge_stream_kernel (default for R <= 64): persistent blocks
+//    stream W through an LDS ring, rank product on the bf16 matrix cores
+//    with fp32 operands split in three bf16 parts;
+//  - lora_merge_mfma_kernel (any R): a block per 128 x 128 tile, rank
+//    product on the fp32 matrix cores (v_mfma_f32_32x32x2_f32);
+//  - lora_merge_split_kernel: the tile-per-block form of the split rank
+//    product (comparisons).
 #include <stdio.h>
 
 #include "hd_common.hpp"
@@ -131,12 +135,368 @@ __global__ __launch_bounds__(256, OCC) void lora_merge_mfma_kernel(uint16_t *__r
     }
 }
 
-// hd_lora_set_family: 0 = the unrolled rank loop (default), 1 = the rolled
-// loop (same-process comparisons; identical results)
+// Split-operand variant on the bf16 matrix cores. Each fp32 operand x is
+// held as three bf16 parts x = x0 + x1 + x2 (x0 = bf16(x), x1 =
+// bf16(x - x0), x2 = bf16(x - x0 - x1); both differences are exact in fp32),
+// and the rank product keeps the six part products down to 2^-16 of the
+// leading one: a0b0 + a0b1 + a1b0 + a0b2 + a1b1 + a2b0 (summed smallest
+// first). What is dropped is below 2^-24 of |ab|, fp32's own rounding level,
+// so the delta matches an fp32 SGEMM up to summation order. Six
+// v_mfma_f32_32x32x16_bf16 per 16 ranks replace eight v_mfma_f32_32x32x2_f32,
+// about 2.7x less matrix-core time: the merge becomes bound by the
+// read-modify-write of W in HBM. Ranks are staged 32 at a time: the six part
+// planes of the up slice [row][r] and of the transposed down slice [col][r]
+// (61 KB) share the LDS with the fp32 delta tile, two blocks per CU.
+#define LS_RC 32
+#define LS_LD (LS_RC + 8)                   // plane row stride (bf16): conflict-free 16-byte reads
+#define LS_PL (LM_T * LS_LD)                // one part plane
+__device__ __forceinline__ void split3(float x, uint16_t &h0, uint16_t &h1, uint16_t &h2) {
+    h0 = f2bf(x);
+    const float r1 = x - bf2f(h0);
+    h1 = f2bf(r1);
+    h2 = f2bf(r1 - bf2f(h1));
+}
+template <int OCC>
+__global__ __launch_bounds__(256, OCC) void lora_merge_split_kernel(uint16_t *__restrict__ w,
+                                                                 const float *__restrict__ up,
+                                                                 const float *__restrict__ down, int N,
+                                                                 int K, int R, float scale) {
+    constexpr int PLANES = 6 * LS_PL * 2, STB = LM_ST * 4;
+    __shared__ __attribute__((aligned(16))) unsigned char lds_raw[PLANES > STB ? PLANES : STB];
+    uint16_t *const pu = (uint16_t *)lds_raw;        // up planes 0..2
+    uint16_t *const pd = pu + 3 * LS_PL;             // down^T planes 0..2
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n0 = blockIdx.y * LM_T, k0 = blockIdx.x * LM_T;
+    const int l32 = lane & 31, lh = lane >> 5;
+    const bool full = n0 + LM_T <= N && k0 + LM_T <= K && K % 8 == 0;
+    u32x4_t wch[8];
+    f32x16_t acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[j][e] = 0.f;
+    // staging roles: up - row ur, ranks ur4 .. ur4+3 (four rows per thread);
+    // down - columns dc4 .. dc4+3, ranks dr4 .. dr4+3
+    const int ur = threadIdx.x / 8, ur4 = (threadIdx.x % 8) * 4;
+    const int dc4 = (threadIdx.x % 32) * 4, dr4 = (threadIdx.x / 32) * 4;
+    for (int r0 = 0; r0 < R; r0 += LS_RC) {
+        float uv[4][4], dv[4][4];   // up: [row block][r]; down: [r][col]
+        const bool fast = full && r0 + LS_RC <= R && R % 4 == 0;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int row = ur + t * 32;
+            if (fast) {
+                const float4 u = *(const float4 *)(up + (size_t)(n0 + row) * R + r0 + ur4);
+                uv[t][0] = u.x; uv[t][1] = u.y; uv[t][2] = u.z; uv[t][3] = u.w;
+                const float4 d = *(const float4 *)(down + (size_t)(r0 + dr4 + t) * K + k0 + dc4);
+                dv[t][0] = d.x; dv[t][1] = d.y; dv[t][2] = d.z; dv[t][3] = d.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int r = r0 + ur4 + e, n = n0 + row;
+                    uv[t][e] = r < R && n < N ? up[(size_t)n * R + r] : 0.f;
+                    const int rd = r0 + dr4 + t, k = k0 + dc4 + e;
+                    dv[t][e] = rd < R && k < K ? down[(size_t)rd * K + k] : 0.f;
+                }
+            }
+        }
+        if (r0 > 0) __syncthreads();   // the previous chunk's planes are read
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            uint16_t h[3][4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) split3(uv[t][e], h[0][e], h[1][e], h[2][e]);
+#pragma unroll
+            for (int p = 0; p < 3; p++) {
+                u32x2_t v = {(uint32_t)h[p][0] | ((uint32_t)h[p][1] << 16),
+                             (uint32_t)h[p][2] | ((uint32_t)h[p][3] << 16)};
+                *(u32x2_t *)(pu + p * LS_PL + (ur + t * 32) * LS_LD + ur4) = v;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {   // column dc4 + e: ranks dr4 .. dr4+3
+            uint16_t h[3][4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) split3(dv[t][e], h[0][t], h[1][t], h[2][t]);
+#pragma unroll
+            for (int p = 0; p < 3; p++) {
+                u32x2_t v = {(uint32_t)h[p][0] | ((uint32_t)h[p][1] << 16),
+                             (uint32_t)h[p][2] | ((uint32_t)h[p][3] << 16)};
+                *(u32x2_t *)(pd + p * LS_PL + (dc4 + e) * LS_LD + dr4) = v;
+            }
+        }
+        __syncthreads();
+        if (r0 == 0 && full) {
+            // W chunks of this thread (8 x 8 weights): issued after the first
+            // rank slice is staged, so that staging does not wait behind
+            // them and their latency hides under the MFMAs
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const int c = threadIdx.x + t * 256, row = c / 16, col = (c % 16) * 8;
+                wch[t] = *(const u32x4_t *)(w + (size_t)(n0 + row) * K + k0 + col);
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < LS_RC / 16; ks++) {
+            const int rr = ks * 16 + lh * 8;
+            bf16x8_t a[3];
+#pragma unroll
+            for (int p = 0; p < 3; p++) a[p] = *(const bf16x8_t *)(pu + p * LS_PL + (wave * 32 + l32) * LS_LD + rr);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                bf16x8_t b[3];
+#pragma unroll
+                for (int p = 0; p < 3; p++) b[p] = *(const bf16x8_t *)(pd + p * LS_PL + (j * 32 + l32) * LS_LD + rr);
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc[j], 0, 0, 0);
+            }
+        }
+    }
+    __syncthreads();   // planes read: the delta tile reuses the LDS
+    float *st = (float *)lds_raw;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+            st[(wave * 32 + (e >> 2) * 8 + lh * 4 + (e & 3)) * (LM_T + 8) + j * 32 + l32] = acc[j][e];
+    __syncthreads();
+    if (full) {
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const int c = threadIdx.x + t * 256, row = c / 16, col = (c % 16) * 8;
+            const float4 d0 = *(const float4 *)(st + row * (LM_T + 8) + col);
+            const float4 d1 = *(const float4 *)(st + row * (LM_T + 8) + col + 4);
+            const float dd[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+            u32x4_t o;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                o[e] = pack_bf2(fmaf(scale, dd[2 * e], lo_bf(wch[t][e])),
+                                fmaf(scale, dd[2 * e + 1], hi_bf(wch[t][e])));
+            *(u32x4_t *)(w + (size_t)(n0 + row) * K + k0 + col) = o;
+        }
+    } else {
+        for (int c = threadIdx.x; c < LM_T * LM_T; c += 256) {
+            const int row = c / LM_T, col = c % LM_T, n = n0 + row, k = k0 + col;
+            if (n < N && k < K) {
+                const size_t o = (size_t)n * K + k;
+                w[o] = f2bf(fmaf(scale, st[row * (LM_T + 8) + col], bf2f(w[o])));
+            }
+        }
+    }
+}
+
+// Streaming merge for R <= 64 (R % 4 == 0, K % 8 == 0): a persistent block of
+// 8 waves per CU walks a contiguous run of 128 x 64 tiles of W (row strips
+// first), so the whole launch is one stream of W reads and writes:
+//  - W tiles go global -> LDS with buffer loads straight to LDS, two tiles
+//    ahead, into a ring of three 16 KB slots; the update reads W from LDS in
+//    the accumulator layout, writes the bf16 result back in place, and the
+//    tile leaves with coalesced 16-byte buffer stores;
+//  - the rank product is the split-operand form of lora_merge_split_kernel
+//    (six bf16 part products per fp32 product); the up strip's part planes
+//    are staged once per row strip, the down slice's once per tile from
+//    registers loaded one tile ahead;
+//  - MFMA A = down^T (rows: W columns k), B = up (columns: W rows n), so a
+//    lane holds four consecutive k of one W row per accumulator group.
+// Every vector memory instruction in the loop is issued unconditionally
+// (offsets past the data read as zero or are dropped), so the counts behind
+// the vmcnt waits hold on every path.
+#define LT_N 128
+#define LT_K 64
+#define LT_LD 72   // plane row stride (bf16): 144-byte rows, conflict-free 16-byte reads
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t lt_rsrc(const void *base, uint32_t nbytes) {
+    const uint64_t b = (uint64_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(((uint64_t)hi << 32) | lo), 0,
+                                             __builtin_amdgcn_readfirstlane(nbytes), 0x00020000);
+}
+__global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__restrict__ w,
+                                                                 const float *__restrict__ up,
+                                                                 const float *__restrict__ down, int N,
+                                                                 int K, int R, float scale, int ntk,
+                                                                 int total) {
+    __shared__ __attribute__((aligned(1024))) uint16_t wring[3][LT_N * LT_K];
+    __shared__ __attribute__((aligned(16))) uint16_t upl[3][LT_N * LT_LD];
+    __shared__ __attribute__((aligned(16))) uint16_t dpl[3][LT_K * LT_LD];
+#if defined(__HIP_DEVICE_COMPILE__)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, lh = lane >> 5;
+    const int tb = (int)((int64_t)blockIdx.x * total / gridDim.x);
+    const int te = (int)((int64_t)(blockIdx.x + 1) * total / gridDim.x);
+    if (tb >= te) return;
+    const uint32_t OOB = 0x80000000u;
+    const __amdgpu_buffer_rsrc_t rw = lt_rsrc(w, (uint32_t)((size_t)N * K * 2));
+    const __amdgpu_buffer_rsrc_t ru = lt_rsrc(up, (uint32_t)((size_t)N * R * 4));
+    // W chunk i (0, 1) of this lane in a tile: LDS slot s = (2 wave + i) 64 +
+    // lane holds 16-byte chunk c = (s % 8) ^ swz(n) of tile row n = s / 8
+    auto w_off = [&](int t, int i) -> uint32_t {
+        const int s = (wave * 2 + i) * 64 + lane, n = s >> 3, c = (s & 7) ^ ((n >> 1) & 7);
+        const int gn = (t / ntk) * LT_N + n, gk = (t % ntk) * LT_K + c * 8;
+        return t < te && gn < N && gk < K ? (uint32_t)(((size_t)gn * K + gk) * 2) : OOB;
+    };
+    auto issue_w = [&](int t) {
+        uint16_t *slot = wring[t % 3];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (HD_LDS void *)(slot + (wave * 2 + i) * 512), 16,
+                                                     w_off(t, i), 0, 0, 0);
+    };
+    // down slice of tile t: ranks rr, rr + 1, columns kc .. kc + 3
+    const int kc = (tid % 16) * 4, rr = (tid / 16) * 2;
+    // issued as assembly: the compiler would otherwise place the wait for
+    // these registers by its own count of the loop's memory operations,
+    // which holds back the W loads issued after them
+    typedef int i32x4_t __attribute__((ext_vector_type(4)));
+    const i32x4_t rd4 = {(int)__builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)down),
+                         (int)__builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)down >> 32)),
+                         (int)__builtin_amdgcn_readfirstlane((uint32_t)((size_t)R * K * 4)), 0x00020000};
+    f32x4_t dreg[2];
+    auto load_down = [&](int t) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int r = rr + j, gk = (t % ntk) * LT_K + kc;
+            const uint32_t o = t < te && r < R && gk < K ? (uint32_t)(((size_t)r * K + gk) * 4) : OOB;
+            asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(dreg[j]) : "v"(o), "s"(rd4) : "memory");
+        }
+    };
+    const int kblk = wave & 1, nblk = wave >> 1;
+    int staged_tn = -1;
+    // prologue: W(tb), down(tb), W(tb + 1); W(t) is always issued before
+    // down(t), so the wait for down(t)'s registers also covers W(t)
+    issue_w(tb);
+    load_down(tb);
+    issue_w(tb + 1);
+    for (int t = tb; t < te; t++) {
+        const int tn = t / ntk;
+        // every wave is done with the previous tile's planes and W slot
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (tn != staged_tn) {
+            // new row strip: the up rows' part planes (rare: drains the queue)
+            const int row = tid / 4, r16 = (tid % 4) * 16, gn = tn * LT_N + row;
+            float uv[16];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int r = r16 + 4 * j;
+                const uint32_t o = gn < N && r < R ? (uint32_t)(((size_t)gn * R + r) * 4) : OOB;
+                const f32x4_t v = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ru, o, 0, 0));
+                uv[4 * j] = v[0]; uv[4 * j + 1] = v[1]; uv[4 * j + 2] = v[2]; uv[4 * j + 3] = v[3];
+            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            uint16_t h[3][16];
+#pragma unroll
+            for (int e = 0; e < 16; e++) split3(uv[e], h[0][e], h[1][e], h[2][e]);
+#pragma unroll
+            for (int pl = 0; pl < 3; pl++)
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    u32x4_t v;
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        v[e] = (uint32_t)h[pl][q * 8 + 2 * e] | ((uint32_t)h[pl][q * 8 + 2 * e + 1] << 16);
+                    *(u32x4_t *)(upl[pl] + row * LT_LD + r16 + q * 8) = v;
+                }
+            staged_tn = tn;
+        }
+        // down(t) registers -> part planes [k][r]. Newer than down(t): W(t+1)
+        // and the previous tile's stores (after a new strip's vmcnt(0):
+        // nothing; the first tile always starts a strip)
+        asm volatile("s_waitcnt vmcnt(4)" : "+v"(dreg[0]), "+v"(dreg[1])::"memory");
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            uint16_t h0[3], h1[3];
+            split3(dreg[0][e], h0[0], h0[1], h0[2]);
+            split3(dreg[1][e], h1[0], h1[1], h1[2]);
+#pragma unroll
+            for (int pl = 0; pl < 3; pl++)
+                *(uint32_t *)(dpl[pl] + (kc + e) * LT_LD + rr) = (uint32_t)h0[pl] | ((uint32_t)h1[pl] << 16);
+        }
+        load_down(t + 1);
+        issue_w(t + 2);
+        // W(t) landed for every wave (at most the 8 newest operations - the
+        // previous tile's stores, down(t+1), W(t+1), W(t+2) - still fly),
+        // planes visible
+        asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        f32x16_t acc;
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[e] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const int rc = ks * 16 + lh * 8;
+            bf16x8_t a[3], b[3];
+#pragma unroll
+            for (int p = 0; p < 3; p++) {
+                a[p] = *(const bf16x8_t *)(dpl[p] + (kblk * 32 + l32) * LT_LD + rc);
+                b[p] = *(const bf16x8_t *)(upl[p] + (nblk * 32 + l32) * LT_LD + rc);
+            }
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc, 0, 0, 0);
+        }
+        // W update in LDS: row n = nblk*32 + l32, columns kblk*32 + 8q + 4lh .. +3.
+        // The ring is touched through assembly only: the compiler would
+        // otherwise wait for every buffer->LDS load in flight (vmcnt(0))
+        // before each access, draining the prefetch; the waits above order
+        // these accesses instead.
+        uint16_t *slot = wring[t % 3];
+        {
+            const int n = nblk * 32 + l32;
+            uint32_t ad[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                ad[q] = (uint32_t)(size_t)(HD_LDS void *)(slot + n * LT_K + (((kblk * 4 + q) ^ ((n >> 1) & 7)) * 8) +
+                                                          lh * 4);
+            u32x2_t wv[4];
+            asm volatile(
+                "ds_read_b64 %0, %4\n\tds_read_b64 %1, %5\n\tds_read_b64 %2, %6\n\tds_read_b64 %3, %7\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=v"(wv[0]), "=v"(wv[1]), "=v"(wv[2]), "=v"(wv[3])
+                : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3])
+                : "memory");
+            u32x2_t o[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                o[q] = (u32x2_t){pack_bf2(fmaf(scale, acc[4 * q], lo_bf(wv[q][0])),
+                                          fmaf(scale, acc[4 * q + 1], hi_bf(wv[q][0]))),
+                                 pack_bf2(fmaf(scale, acc[4 * q + 2], lo_bf(wv[q][1])),
+                                          fmaf(scale, acc[4 * q + 3], hi_bf(wv[q][1])))};
+            asm volatile(
+                "ds_write_b64 %0, %1\n\tds_write_b64 %2, %3\n\tds_write_b64 %4, %5\n\tds_write_b64 %6, %7"
+                :
+                : "v"(ad[0]), "v"(o[0]), "v"(ad[1]), "v"(o[1]), "v"(ad[2]), "v"(o[2]), "v"(ad[3]), "v"(o[3])
+                : "memory");
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        // the tile leaves in the chunk order it arrived in
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t sa = (uint32_t)(size_t)(HD_LDS void *)(slot + ((wave * 2 + i) * 64 + lane) * 8);
+            u32x4_t v;
+            asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(sa) : "memory");
+            __builtin_amdgcn_raw_buffer_store_b128(v, rw, w_off(t, i), 0, 0);
+        }
+    }
+    // no LDS-bound load may land after the block ends
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#endif
+}
+
+// hd_lora_set_family: 0 = the streaming split-operand kernel where it
+// applies (R <= 64, R % 4 == 0, K % 8 == 0, W under 2 GiB), else the fp32
+// matrix-core kernel (default); 1 = always the fp32 matrix-core kernel with
+// the unrolled rank loop; 2 = the same with the rolled loop; 3 = the
+// one-tile-per-block split-operand kernel (same-process comparisons)
 static int g_lora_family = 0;
 extern "C" int hd_lora_set_family(int family) {
     const int prev = g_lora_family;
-    g_lora_family = family == 1 ? 1 : 0;
+    g_lora_family = family >= 1 && family <= 3 ? family : 0;
     return prev;
 }
 
@@ -161,12 +521,26 @@ extern "C" hd_status hd_lora_merge_gpu(hd_lora_entry *entries, size_t count, voi
         const int N = (int)e->out_dim, K = (int)e->in_dim, R = (int)e->rank;
         const float scale = e->multiplier * e->alpha / (float)e->rank;   // lora_merge.cu:54
         dim3 grid(hd_cdiv(K, LM_T), hd_cdiv(N, LM_T));
-        if (g_lora_family == 1)
+        const bool stream_ok = R <= 64 && R % 4 == 0 && K % 8 == 0 && (size_t)N * K * 2 < ((size_t)1 << 31);
+        if (g_lora_family == 0 && stream_ok) {
+            const int ntk = hd_cdiv(K, LT_K), total = hd_cdiv(N, LT_N) * ntk;
+            int cus = 0, dev = 0;
+            if (hipGetDevice(&dev) != hipSuccess ||
+                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+                cus = 256;
+            lora_merge_stream_kernel<<<total < cus ? total : cus, 512, 0, st>>>(
+                (uint16_t *)e->base_dev, (const float *)e->up_dev, (const float *)e->down_dev, N, K, R, scale,
+                ntk, total);
+        } else if (g_lora_family == 3) {
+            lora_merge_split_kernel<2><<<grid, 256, 0, st>>>((uint16_t *)e->base_dev, (const float *)e->up_dev,
+                                                             (const float *)e->down_dev, N, K, R, scale);
+        } else if (g_lora_family == 2) {
             lora_merge_mfma_kernel<2, false><<<grid, 256, 0, st>>>((uint16_t *)e->base_dev, (const float *)e->up_dev,
                                                             (const float *)e->down_dev, N, K, R, scale);
-        else
+        } else {
             lora_merge_mfma_kernel<2><<<grid, 256, 0, st>>>((uint16_t *)e->base_dev, (const float *)e->up_dev,
                                                             (const float *)e->down_dev, N, K, R, scale);
+        }
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) {
             hd_set_error("lora: merge launch failed: %s", hipGetErrorString(err));

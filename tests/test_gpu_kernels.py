@@ -651,3 +651,42 @@ def test_patchify_bf16_and_rotary_scalar_path(pkg, lib, dev):
     lib.hd_apply_rotary(pkg.ptr(xd), pkg.ptr(cd), pkg.ptr(sd), pkg.ptr(y), 2, seq, dim)
     torch.cuda.synchronize()
     assert np.array_equal(host(y), orc.apply_rotary(x, cr, sr, 1))
+
+
+@pytest.mark.parametrize("N,K,R", [(300, 520, 64), (257, 136, 36), (4224, 1032, 64), (130, 72, 8),
+                                   (300, 520, 37), (520, 264, 128)])
+def test_lora_merge_families(pkg, lib, dev, N, K, R):
+    """The merge kernels against each other and the fp32 oracle: the
+    streaming split-operand kernel (default for rank <= 64, rank % 4 == 0)
+    equals its one-tile-per-block form bit for bit (same products, same
+    summation order), including ragged tiles and row strips that cross the
+    persistent blocks' ranges; ranks it does not take (37, 128) run the fp32
+    matrix-core kernel under the default family. Every family stays within
+    one bf16 step of the oracle (lora_merge.cu:35-104)."""
+    rng = np.random.default_rng(N * 7 + K + R)
+    w = orc.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 0.02)
+    up = (rng.standard_normal((N, R)) * 0.01).astype(np.float32)
+    down = (rng.standard_normal((R, K)) * 0.01).astype(np.float32)
+    upd, dnd = torch.from_numpy(up).to(dev), torch.from_numpy(down).to(dev)
+    ref = orc.lora_merge(w, up, down, 0.75)
+    outs = {}
+    prev = lib.hd_lora_set_family(0)
+    try:
+        for fam in (0, 1, 3):
+            lib.hd_lora_set_family(fam)
+            wd = dbf(w, dev)
+            e = pkg.hd_lora_entry()
+            e.rank, e.in_dim, e.out_dim, e.alpha, e.multiplier = R, K, N, float(R), 0.75
+            e.down_dev, e.up_dev, e.base_dev = dnd.data_ptr(), upd.data_ptr(), wd.data_ptr()
+            assert lib.hd_lora_merge_gpu(ctypes.byref(e), 1, None) == 0
+            torch.cuda.synchronize()
+            outs[fam] = host(wd)
+    finally:
+        lib.hd_lora_set_family(prev)
+    for fam, got in outs.items():
+        assert close_bf16(got, ref, ulps=1, atol_rel=1e-4), fam
+        assert np.mean(got == ref) > 0.999, fam
+    if R <= 64 and R % 4 == 0:
+        assert np.array_equal(outs[0], outs[3])
+    else:
+        assert np.array_equal(outs[0], outs[1])
