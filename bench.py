@@ -499,6 +499,15 @@ def run_c4(pkg, lib, model, tensors, cfg, ws, ids, posd, vin, T, I, S, dev, args
             e.rank, e.in_dim, e.out_dim, e.alpha, e.multiplier = r, K, N, float(r), 1.0
             e.up_dev, e.down_dev, e.base_dev = up.data_ptr(), down.data_ptr(), w.data_ptr()
             k += 1
+    # one merge into a small scratch weight first, so the timed call does
+    # not include loading the kernels' code on their first launch
+    wx = torch.zeros(256, 256, dtype=torch.bfloat16, device=dev)
+    ux, dx = torch.zeros(256, r, device=dev), torch.zeros(r, 256, device=dev)
+    ex = pkg.hd_lora_entry()
+    ex.rank, ex.in_dim, ex.out_dim, ex.alpha, ex.multiplier = r, 256, 256, float(r), 1.0
+    ex.up_dev, ex.down_dev, ex.base_dev = ux.data_ptr(), dx.data_ptr(), wx.data_ptr()
+    if lib.hd_lora_merge_gpu(ctypes.byref(ex), 1, None) != 0:
+        raise RuntimeError(lib.hd_last_error().decode())
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()

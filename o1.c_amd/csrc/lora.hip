@@ -298,13 +298,15 @@ __global__ __launch_bounds__(256, OCC) void lora_merge_split_kernel(uint16_t *__
 //    tile leaves with coalesced 16-byte buffer stores;
 //  - the rank product is the split-operand form of lora_merge_split_kernel
 //    (six bf16 part products per fp32 product); the up strip's part planes
-//    are staged once per row strip, the down slice's once per tile from
-//    registers loaded one tile ahead;
+//    are staged once per row strip, the down slice's once per tile, into one
+//    of two plane buffers, from registers loaded a tile ahead, while the
+//    previous tile's MFMAs run (two barriers per tile);
 //  - MFMA A = down^T (rows: W columns k), B = up (columns: W rows n), so a
 //    lane holds four consecutive k of one W row per accumulator group.
 // Every vector memory instruction in the loop is issued unconditionally
 // (offsets past the data read as zero or are dropped), so the counts behind
-// the vmcnt waits hold on every path.
+// the hand-placed vmcnt waits for the ring hold on every path; register
+// loads go through the compiler, which places their waits.
 #define LT_N 128
 #define LT_K 64
 #define LT_LD 72   // plane row stride (bf16): 144-byte rows, conflict-free 16-byte reads
@@ -322,7 +324,7 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
                                                                  int total) {
     __shared__ __attribute__((aligned(1024))) uint16_t wring[3][LT_N * LT_K];
     __shared__ __attribute__((aligned(16))) uint16_t upl[3][LT_N * LT_LD];
-    __shared__ __attribute__((aligned(16))) uint16_t dpl[3][LT_K * LT_LD];
+    __shared__ __attribute__((aligned(16))) uint16_t dpl[2][3][LT_K * LT_LD];
 #if defined(__HIP_DEVICE_COMPILE__)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, lh = lane >> 5;
@@ -334,10 +336,16 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
     const __amdgpu_buffer_rsrc_t ru = lt_rsrc(up, (uint32_t)((size_t)N * R * 4));
     // W chunk i (0, 1) of this lane in a tile: LDS slot s = (2 wave + i) 64 +
     // lane holds 16-byte chunk c = (s % 8) ^ swz(n) of tile row n = s / 8
+    int wn[2], wc[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int s = (wave * 2 + i) * 64 + lane;
+        wn[i] = s >> 3;
+        wc[i] = ((s & 7) ^ ((wn[i] >> 1) & 7)) * 8;
+    }
     auto w_off = [&](int t, int i) -> uint32_t {
-        const int s = (wave * 2 + i) * 64 + lane, n = s >> 3, c = (s & 7) ^ ((n >> 1) & 7);
-        const int gn = (t / ntk) * LT_N + n, gk = (t % ntk) * LT_K + c * 8;
-        return t < te && gn < N && gk < K ? (uint32_t)(((size_t)gn * K + gk) * 2) : OOB;
+        const int gn = (t / ntk) * LT_N + wn[i], gk = (t % ntk) * LT_K + wc[i];
+        return t < te && gn < N && gk < K ? (uint32_t)(gn * K + gk) * 2u : OOB;
     };
     auto issue_w = [&](int t) {
         uint16_t *slot = wring[t % 3];
@@ -346,100 +354,108 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (HD_LDS void *)(slot + (wave * 2 + i) * 512), 16,
                                                      w_off(t, i), 0, 0, 0);
     };
-    // down slice of tile t: ranks rr, rr + 1, columns kc .. kc + 3
+    // down slice of a tile: ranks rr, rr + 1, columns kc .. kc + 3
+    const __amdgpu_buffer_rsrc_t rd = lt_rsrc(down, (uint32_t)((size_t)R * K * 4));
     const int kc = (tid % 16) * 4, rr = (tid / 16) * 2;
-    // issued as assembly: the compiler would otherwise place the wait for
-    // these registers by its own count of the loop's memory operations,
-    // which holds back the W loads issued after them
-    typedef int i32x4_t __attribute__((ext_vector_type(4)));
-    const i32x4_t rd4 = {(int)__builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)down),
-                         (int)__builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)down >> 32)),
-                         (int)__builtin_amdgcn_readfirstlane((uint32_t)((size_t)R * K * 4)), 0x00020000};
-    f32x4_t dreg[2];
-    auto load_down = [&](int t) {
+    f32x4_t DA[2], DB[2];
+    auto load_down = [&](int t, f32x4_t (&d)[2]) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int r = rr + j, gk = (t % ntk) * LT_K + kc;
-            const uint32_t o = t < te && r < R && gk < K ? (uint32_t)(((size_t)r * K + gk) * 4) : OOB;
-            asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(dreg[j]) : "v"(o), "s"(rd4) : "memory");
+            const uint32_t o = t < te && r < R && gk < K ? (uint32_t)(r * K + gk) * 4u : OOB;
+            d[j] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rd, o, 0, 0));
         }
     };
-    const int kblk = wave & 1, nblk = wave >> 1;
-    int staged_tn = -1;
-    // prologue: W(tb), down(tb), W(tb + 1); W(t) is always issued before
-    // down(t), so the wait for down(t)'s registers also covers W(t)
-    issue_w(tb);
-    load_down(tb);
-    issue_w(tb + 1);
-    for (int t = tb; t < te; t++) {
-        const int tn = t / ntk;
-        // every wave is done with the previous tile's planes and W slot
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (tn != staged_tn) {
-            // new row strip: the up rows' part planes (rare: drains the queue)
-            const int row = tid / 4, r16 = (tid % 4) * 16, gn = tn * LT_N + row;
-            float uv[16];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int r = r16 + 4 * j;
-                const uint32_t o = gn < N && r < R ? (uint32_t)(((size_t)gn * R + r) * 4) : OOB;
-                const f32x4_t v = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ru, o, 0, 0));
-                uv[4 * j] = v[0]; uv[4 * j + 1] = v[1]; uv[4 * j + 2] = v[2]; uv[4 * j + 3] = v[3];
-            }
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            uint16_t h[3][16];
-#pragma unroll
-            for (int e = 0; e < 16; e++) split3(uv[e], h[0][e], h[1][e], h[2][e]);
-#pragma unroll
-            for (int pl = 0; pl < 3; pl++)
-#pragma unroll
-                for (int q = 0; q < 2; q++) {
-                    u32x4_t v;
-#pragma unroll
-                    for (int e = 0; e < 4; e++)
-                        v[e] = (uint32_t)h[pl][q * 8 + 2 * e] | ((uint32_t)h[pl][q * 8 + 2 * e + 1] << 16);
-                    *(u32x4_t *)(upl[pl] + row * LT_LD + r16 + q * 8) = v;
-                }
-            staged_tn = tn;
-        }
-        // down(t) registers -> part planes [k][r]. Newer than down(t): W(t+1)
-        // and the previous tile's stores (after a new strip's vmcnt(0):
-        // nothing; the first tile always starts a strip)
-        asm volatile("s_waitcnt vmcnt(4)" : "+v"(dreg[0]), "+v"(dreg[1])::"memory");
+    // down registers -> part planes [k][r] of buffer b
+    auto put_down = [&](const f32x4_t (&d)[2], int b) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             uint16_t h0[3], h1[3];
-            split3(dreg[0][e], h0[0], h0[1], h0[2]);
-            split3(dreg[1][e], h1[0], h1[1], h1[2]);
+            split3(d[0][e], h0[0], h0[1], h0[2]);
+            split3(d[1][e], h1[0], h1[1], h1[2]);
 #pragma unroll
             for (int pl = 0; pl < 3; pl++)
-                *(uint32_t *)(dpl[pl] + (kc + e) * LT_LD + rr) = (uint32_t)h0[pl] | ((uint32_t)h1[pl] << 16);
+                *(uint32_t *)(dpl[b][pl] + (kc + e) * LT_LD + rr) = (uint32_t)h0[pl] | ((uint32_t)h1[pl] << 16);
         }
-        load_down(t + 1);
-        issue_w(t + 2);
-        // W(t) landed for every wave (at most the 8 newest operations - the
-        // previous tile's stores, down(t+1), W(t+1), W(t+2) - still fly),
-        // planes visible
+    };
+    auto stage_up = [&](int tn) {   // the up strip's part planes; drains the queue
+        const int row = tid / 4, r16 = (tid % 4) * 16, gn = tn * LT_N + row;
+        float uv[16];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r = r16 + 4 * j;
+            const uint32_t o = gn < N && r < R ? (uint32_t)(gn * R + r) * 4u : OOB;
+            const f32x4_t v = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ru, o, 0, 0));
+            uv[4 * j] = v[0]; uv[4 * j + 1] = v[1]; uv[4 * j + 2] = v[2]; uv[4 * j + 3] = v[3];
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        uint16_t h[3][16];
+#pragma unroll
+        for (int e = 0; e < 16; e++) split3(uv[e], h[0][e], h[1][e], h[2][e]);
+#pragma unroll
+        for (int pl = 0; pl < 3; pl++)
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                u32x4_t v;
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    v[e] = (uint32_t)h[pl][q * 8 + 2 * e] | ((uint32_t)h[pl][q * 8 + 2 * e + 1] << 16);
+                *(u32x4_t *)(upl[pl] + row * LT_LD + r16 + q * 8) = v;
+            }
+    };
+    const int kblk = wave & 1, nblk = wave >> 1;
+    // prologue: W(tb), down(tb), W(tb+1), down(tb+1); the planes of tile tb
+    issue_w(tb);
+    load_down(tb, DA);
+    issue_w(tb + 1);
+    load_down(tb + 1, DB);
+    int staged_tn = tb / ntk;
+    stage_up(staged_tn);   // vmcnt(0): down(tb) landed as well
+    put_down(DA, tb & 1);
+    // tile t splits down(t+1) (registers dsplit) for the next tile and loads
+    // down(t+2) into the registers down(t) used (dload); the loop runs two
+    // tiles per trip with the two register sets swapped, so no register
+    // holding a load in flight is ever copied
+    auto step = [&](int t, const f32x4_t (&dsplit)[2], f32x4_t (&dload)[2]) {
+        // W(t) landed for every wave (newer than W(t): down(t), the stores of
+        // t-2, W(t+1), down(t+1), the stores of t-1 - ten operations, or a
+        // full drain since); the planes of tile t are written; every wave is
+        // past the previous tile's store pass (its ring slot is free) and
+        // MFMAs (the other plane buffer is free)
         asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const int tn = t / ntk;
+        if (tn != staged_tn) {
+            stage_up(tn);
+            staged_tn = tn;
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        }
+        // the MFMAs of tile t; the next tile's down slice is split into the
+        // other plane buffer in between (independent VALU and LDS work)
+        const int b = t & 1;
         f32x16_t acc;
 #pragma unroll
         for (int e = 0; e < 16; e++) acc[e] = 0.f;
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             const int rc = ks * 16 + lh * 8;
-            bf16x8_t a[3], b[3];
+            bf16x8_t a[3], bb[3];
 #pragma unroll
             for (int p = 0; p < 3; p++) {
-                a[p] = *(const bf16x8_t *)(dpl[p] + (kblk * 32 + l32) * LT_LD + rc);
-                b[p] = *(const bf16x8_t *)(upl[p] + (nblk * 32 + l32) * LT_LD + rc);
+                a[p] = *(const bf16x8_t *)(dpl[b][p] + (kblk * 32 + l32) * LT_LD + rc);
+                bb[p] = *(const bf16x8_t *)(upl[p] + (nblk * 32 + l32) * LT_LD + rc);
             }
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], bb[0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], bb[1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], bb[2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], bb[0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], bb[1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], bb[0], acc, 0, 0, 0);
+            if (ks == 1) put_down(dsplit, b ^ 1);
         }
+        // loads for two tiles ahead, issued after down(t+1)'s registers are
+        // consumed so that waiting for those never waits for these
+        issue_w(t + 2);
+        load_down(t + 2, dload);
         // W update in LDS: row n = nblk*32 + l32, columns kblk*32 + 8q + 4lh .. +3.
         // The ring is touched through assembly only: the compiler would
         // otherwise wait for every buffer->LDS load in flight (vmcnt(0))
@@ -482,6 +498,10 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
             asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(sa) : "memory");
             __builtin_amdgcn_raw_buffer_store_b128(v, rw, w_off(t, i), 0, 0);
         }
+    };
+    for (int t = tb; t < te; t += 2) {
+        step(t, DB, DA);
+        if (t + 1 < te) step(t + 1, DA, DB);
     }
     // no LDS-bound load may land after the block ends
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
