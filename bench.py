@@ -109,9 +109,13 @@ def main():
         kk = torch.randn(B, NKV, S, D, device=dev).to(torch.bfloat16)
         vt = torch.randn(lib.hd_flash_vt_bytes(B, NKV, S) // 2, device=dev).to(torch.bfloat16)
         ao = torch.empty(B, S, NH * D, dtype=torch.bfloat16, device=dev)
+        # with the tail-split workspace, as the decoder block launches it
+        fws = torch.empty(lib.hd_flash_ws_bytes(), dtype=torch.uint8, device=dev)
         for _ in range(args.kernel_iters):
-            lib.hd_flash_attention(pkg.ptr(q), pkg.ptr(kk), pkg.ptr(vt), None, pkg.ptr(ao), B, NH, NKV,
-                                   S, D, 0, D ** -0.5, 1)
+            rc = lib.hd_flash_attention_ws(pkg.ptr(q), pkg.ptr(kk), pkg.ptr(vt), None, pkg.ptr(ao), B, NH,
+                                           NKV, S, D, 0, D ** -0.5, 1, pkg.ptr(fws), fws.numel())
+            if rc != 0:
+                raise RuntimeError(lib.hd_cuda_last_error().decode())
         torch.cuda.synchronize()
         return
     if args.vision_only:
