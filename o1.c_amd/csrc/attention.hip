@@ -46,6 +46,7 @@ struct FaArgs {
     uint16_t *out;         // seq-major [B,S,Hq*D] or head-major [B,Hq,S,D]
     int S, S_pad, Hq, Hkv;
     int ar_len;            // rows < ar_len: causal
+    int q_row_begin;       // first query row of the launch (its q tiles start here)
     int q_row_end;         // only rows < q_row_end are computed/written
     float scale_log2;      // scale * log2(e)
     float inv_scale;       // 1 / scale (mask values are added to raw scores)
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(NWV * 64, 8 / NWV) void flash_fwd_kernel(FaArgs a) 
 
     // block -> (b, head, q tile). Query heads sharing one kv head get
     // consecutive linear ids so they run close together in time.
-    const int nqt = (a.q_row_end + BQ - 1) / BQ;
+    const int nqt = (a.q_row_end - a.q_row_begin + BQ - 1) / BQ;
     const int group = a.Hq / a.Hkv;
     int lin = blockIdx.x, chunk = -1, item = 0;
     if (lin >= a.n_whole) {
@@ -122,13 +123,14 @@ __global__ __launch_bounds__(NWV * 64, 8 / NWV) void flash_fwd_kernel(FaArgs a) 
     const int b = lin / a.Hkv;
     const int hq = hk * group + g;
 
-    const int q0 = qt * BQ + wave * 32;
+    const int qb = a.q_row_begin + qt * BQ;          // the block's first query row
+    const int q0 = qb + wave * 32;
     const int my_q = q0 + l32;                       // this lane's query row
-    const bool causal_block = (qt * BQ) < a.ar_len;
+    const bool causal_block = qb < a.ar_len;
     // keys needed by this block
     int kv_end = a.S;
     if (causal_block) {
-        int last_row = min(qt * BQ + BQ, a.q_row_end) - 1;
+        int last_row = min(qb + BQ, a.q_row_end) - 1;
         if (last_row < a.ar_len) kv_end = last_row + 1;
     }
     int t_begin = 0, t_end = (kv_end + FA_BK - 1) / FA_BK;
@@ -218,21 +220,28 @@ __global__ __launch_bounds__(NWV * 64, 8 / NWV) void flash_fwd_kernel(FaArgs a) 
         const bool need_mask = MASKED && (a.mask != nullptr || kv0 + FA_BK > a.S ||
                                           (q0 < a.ar_len && kv0 + FA_BK - 1 > q0));
         float mt = -INFINITY;
+        // the wave-uniform test is taken once per tile, so tiles without
+        // masked keys run exactly the unmasked kernel's max loop
+        if (need_mask) {
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+            for (int j = 0; j < 2; j++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                float v = s[j][r];
-                if (need_mask) {
+                for (int r = 0; r < 16; r++) {
+                    float v = s[j][r];
                     const int kv = kv0 + j * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
                     bool dead = kv >= a.S || (my_q < a.ar_len && kv > my_q);
                     if (a.mask && !dead && my_q < a.S)
                         v += bf2f(a.mask[(size_t)my_q * a.S + kv]) * a.inv_scale;
                     if (dead) v = -INFINITY;
                     s[j][r] = v;
+                    mt = fmaxf(mt, v);
                 }
-                mt = fmaxf(mt, v);
-            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) mt = fmaxf(mt, s[j][r]);
+        }
         mt = xor32_max(mt);
         // Lazy rescale: the running max only moves when some row's tile max
         // exceeds it by more than 2^FA_TAU in probability terms, so the O
@@ -355,12 +364,12 @@ __global__ __launch_bounds__(256) void fa_merge_kernel(FaArgs a, int n_tail) {
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[e] = fmaf(w, pv[e], acc[e]);
     }
-    const int nqt = (a.q_row_end + BQ - 1) / BQ, group = a.Hq / a.Hkv;
+    const int nqt = (a.q_row_end - a.q_row_begin + BQ - 1) / BQ, group = a.Hq / a.Hkv;
     int lin = a.n_whole + tu;
     const int g = lin % group; lin /= group;
     const int qt = lin % nqt; lin /= nqt;
     const int hk = lin % a.Hkv, b = lin / a.Hkv, hq = hk * group + g;
-    const int my_q = qt * BQ + row;
+    const int my_q = a.q_row_begin + qt * BQ + row;
     if (my_q >= a.q_row_end) return;
     const size_t o = a.out_seq_major ? (((size_t)b * a.out_rows + my_q) * a.Hq + hq) * FA_D + d0
                                      : (((size_t)b * a.Hq + hq) * a.out_rows + my_q) * FA_D + d0;
@@ -427,7 +436,21 @@ extern "C" void hd_flash_make_vt(const void *v, void *vt, int bh, int seq) {
 static int fa_launch(const void *q, const void *k, const void *vt, const void *mask, void *out,
                      int batch, int hq, int hkv, int seq, int ar_len, int q_row_end, float scale,
                      int out_seq_major, hipStream_t st, void *ws = nullptr, int64_t ws_bytes = 0,
-                     int out_rows = 0) {
+                     int out_rows = 0, int q_row_begin = 0) {
+    // A causal text prefix (rows < ar_len see keys <= row) over full
+    // attention below it: the prefix rows run as a masked launch of their
+    // own, whose blocks all end at their diagonal, and rows ar_len.. are plain
+    // full attention in the unmasked kernel with the tail split. One masked
+    // launch over all rows costs 7-12 % more: its block holding row ar_len
+    // runs every key with most of its waves masked, and it has no split.
+    if (ar_len > 0 && !mask && ws && q_row_begin == 0 && (seq % FA_BK) == 0 && ar_len < q_row_end &&
+        g_fa_family == 0) {
+        const int rc = fa_launch(q, k, vt, nullptr, out, batch, hq, hkv, seq, ar_len, ar_len, scale,
+                                 out_seq_major, st, nullptr, 0, out_rows, 0);
+        if (rc) return rc;
+        return fa_launch(q, k, vt, nullptr, out, batch, hq, hkv, seq, 0, q_row_end, scale, out_seq_major, st,
+                         ws, ws_bytes, out_rows, ar_len);
+    }
     FaArgs a;
     a.q = (const uint16_t *)q;
     a.k = (const uint16_t *)k;
@@ -439,6 +462,7 @@ static int fa_launch(const void *q, const void *k, const void *vt, const void *m
     a.Hq = hq;
     a.Hkv = hkv;
     a.ar_len = ar_len;
+    a.q_row_begin = q_row_begin;
     a.q_row_end = q_row_end;
     a.scale_log2 = scale * 1.44269504088896341f;
     a.inv_scale = 1.0f / scale;
@@ -451,7 +475,7 @@ static int fa_launch(const void *q, const void *k, const void *vt, const void *m
     const bool split_ok = ws && !mask && ar_len == 0;
     const int nwv = g_fa_family == 1 ? 4 : g_fa_family == 2 ? 8 : (split_ok && seq >= 1024 ? 8 : 4);
     const int BQ = nwv * 32;
-    const int nqt = (q_row_end + BQ - 1) / BQ;
+    const int nqt = (q_row_end - q_row_begin + BQ - 1) / BQ;
     const int units = batch * hq * nqt;
     bool masked = mask || ar_len > 0 || (seq % FA_BK) != 0;
     // Tail split (full attention only): the units of the last partial round

@@ -690,3 +690,41 @@ def test_lora_merge_families(pkg, lib, dev, N, K, R):
         assert np.array_equal(outs[0], outs[3])
     else:
         assert np.array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("B,S,T", [(1, 1152, 128), (2, 640, 300), (1, 2176, 65), (1, 4352, 256)])
+def test_flash_causal_prefix_split_launch(pkg, lib, dev, B, S, T):
+    """A causal text prefix (rows < ar_len = T - 1 see keys <= row) with the
+    tail-split workspace runs as two launches: the prefix rows masked, the
+    rows from ar_len on as full attention with a query-row offset and the
+    tail split (hd_cudnn_sdpa.cu:376-441 runs the same split as two cuDNN
+    passes). Checked against an fp32 torch statement of the attention with
+    that mask, and against the single masked launch (no workspace)."""
+    g = torch.Generator(device=dev).manual_seed(S + T)
+    q = torch.randn(B, 32, S, 128, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(B, 8, S, 128, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(B * 8, S, 128, generator=g, device=dev).to(torch.bfloat16)
+    vt = torch.empty(lib.hd_flash_vt_bytes(B, 8, S) // 2, dtype=torch.bfloat16, device=dev)
+    lib.hd_flash_make_vt(pkg.ptr(v), pkg.ptr(vt), B * 8, S)
+    ws = torch.empty(lib.hd_flash_ws_bytes(), dtype=torch.uint8, device=dev)
+    ar = T - 1
+    o_split = torch.zeros(B, S, 32 * 128, dtype=torch.bfloat16, device=dev)
+    o_one = torch.zeros_like(o_split)
+    assert lib.hd_flash_attention_ws(pkg.ptr(q), pkg.ptr(k), pkg.ptr(vt), None, pkg.ptr(o_split), B, 32, 8, S,
+                                     128, ar, 128 ** -0.5, 1, pkg.ptr(ws), ws.numel()) == 0
+    assert lib.hd_flash_attention(pkg.ptr(q), pkg.ptr(k), pkg.ptr(vt), None, pkg.ptr(o_one), B, 32, 8, S, 128,
+                                  ar, 128 ** -0.5, 1) == 0
+    torch.cuda.synchronize()
+    qf = q.float()
+    kf = k.float().repeat_interleave(4, 1)
+    vf = v.float().view(B, 8, S, 128).repeat_interleave(4, 1)
+    sc = qf @ kf.transpose(-1, -2) * 128 ** -0.5
+    i = torch.arange(S, device=dev)
+    sc = sc.masked_fill((i[:, None] < ar) & (i[None, :] > i[:, None]), float("-inf"))
+    ref = (torch.softmax(sc, -1) @ vf).permute(0, 2, 1, 3).reshape(B, S, 32 * 128)
+    for got in (o_split, o_one):
+        gf = got.float()
+        assert float((gf - ref).norm() / ref.norm()) < 5e-3
+        assert float((gf[:, :ar] - ref[:, :ar]).norm() / ref[:, :ar].norm()) < 5e-3
+    # the prefix rows come from the same masked kernel either way
+    assert torch.equal(o_split[:, :ar], o_one[:, :ar])
