@@ -343,26 +343,42 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
         wn[i] = s >> 3;
         wc[i] = ((s & 7) ^ ((wn[i] >> 1) & 7)) * 8;
     }
-    auto w_off = [&](int t, int i) -> uint32_t {
-        const int gn = (t / ntk) * LT_N + wn[i], gk = (t % ntk) * LT_K + wc[i];
-        return t < te && gn < N && gk < K ? (uint32_t)(gn * K + gk) * 2u : OOB;
+    // tile coordinates (row strip, column tile) and ring slots advance
+    // incrementally: a division by the runtime ntk costs tens of scalar
+    // instructions, and every wave needs them for three tiles per step
+    struct TC {
+        int tn, tk;
+        bool ok;   // the tile exists (t < te)
     };
-    auto issue_w = [&](int t) {
-        uint16_t *slot = wring[t % 3];
+    auto tc_next = [&](TC c, int t_next) {
+        c.tk++;
+        if (c.tk == ntk) {
+            c.tk = 0;
+            c.tn++;
+        }
+        c.ok = t_next < te;
+        return c;
+    };
+    auto w_off = [&](const TC &c, int i) -> uint32_t {
+        const int gn = c.tn * LT_N + wn[i], gk = c.tk * LT_K + wc[i];
+        return c.ok && gn < N && gk < K ? (uint32_t)(gn * K + gk) * 2u : OOB;
+    };
+    auto issue_w = [&](const TC &c, int sl) {
+        uint16_t *slot = wring[sl];
 #pragma unroll
         for (int i = 0; i < 2; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (HD_LDS void *)(slot + (wave * 2 + i) * 512), 16,
-                                                     w_off(t, i), 0, 0, 0);
+                                                     w_off(c, i), 0, 0, 0);
     };
     // down slice of a tile: ranks rr, rr + 1, columns kc .. kc + 3
     const __amdgpu_buffer_rsrc_t rd = lt_rsrc(down, (uint32_t)((size_t)R * K * 4));
     const int kc = (tid % 16) * 4, rr = (tid / 16) * 2;
     f32x4_t DA[2], DB[2];
-    auto load_down = [&](int t, f32x4_t (&d)[2]) {
+    auto load_down = [&](const TC &c, f32x4_t (&d)[2]) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            const int r = rr + j, gk = (t % ntk) * LT_K + kc;
-            const uint32_t o = t < te && r < R && gk < K ? (uint32_t)(r * K + gk) * 4u : OOB;
+            const int r = rr + j, gk = c.tk * LT_K + kc;
+            const uint32_t o = c.ok && r < R && gk < K ? (uint32_t)(r * K + gk) * 4u : OOB;
             d[j] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rd, o, 0, 0));
         }
     };
@@ -405,11 +421,15 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
     };
     const int kblk = wave & 1, nblk = wave >> 1;
     // prologue: W(tb), down(tb), W(tb+1), down(tb+1); the planes of tile tb
-    issue_w(tb);
-    load_down(tb, DA);
-    issue_w(tb + 1);
-    load_down(tb + 1, DB);
-    int staged_tn = tb / ntk;
+    TC c0 = {tb / ntk, tb % ntk, true};   // tile t
+    TC c1 = tc_next(c0, tb + 1);          // tile t + 1
+    TC c2 = tc_next(c1, tb + 2);          // tile t + 2
+    int sl = 0;                           // ring slot of tile t
+    issue_w(c0, 0);
+    load_down(c0, DA);
+    issue_w(c1, 1);
+    load_down(c1, DB);
+    int staged_tn = c0.tn;
     stage_up(staged_tn);   // vmcnt(0): down(tb) landed as well
     put_down(DA, tb & 1);
     // tile t splits down(t+1) (registers dsplit) for the next tile and loads
@@ -423,10 +443,9 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
         // past the previous tile's store pass (its ring slot is free) and
         // MFMAs (the other plane buffer is free)
         asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        const int tn = t / ntk;
-        if (tn != staged_tn) {
-            stage_up(tn);
-            staged_tn = tn;
+        if (c0.tn != staged_tn) {
+            stage_up(c0.tn);
+            staged_tn = c0.tn;
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         }
         // the MFMAs of tile t; the next tile's down slice is split into the
@@ -454,14 +473,15 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
         }
         // loads for two tiles ahead, issued after down(t+1)'s registers are
         // consumed so that waiting for those never waits for these
-        issue_w(t + 2);
-        load_down(t + 2, dload);
+        const int sl2 = sl == 0 ? 2 : sl - 1;   // tile t+2 takes the slot tile t-1 used
+        issue_w(c2, sl2);
+        load_down(c2, dload);
         // W update in LDS: row n = nblk*32 + l32, columns kblk*32 + 8q + 4lh .. +3.
         // The ring is touched through assembly only: the compiler would
         // otherwise wait for every buffer->LDS load in flight (vmcnt(0))
         // before each access, draining the prefetch; the waits above order
         // these accesses instead.
-        uint16_t *slot = wring[t % 3];
+        uint16_t *slot = wring[sl];
         {
             const int n = nblk * 32 + l32;
             uint32_t ad[4];
@@ -496,8 +516,12 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
             const uint32_t sa = (uint32_t)(size_t)(HD_LDS void *)(slot + ((wave * 2 + i) * 64 + lane) * 8);
             u32x4_t v;
             asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(sa) : "memory");
-            __builtin_amdgcn_raw_buffer_store_b128(v, rw, w_off(t, i), 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(v, rw, w_off(c0, i), 0, 0);
         }
+        c0 = c1;
+        c1 = c2;
+        c2 = tc_next(c2, t + 3);
+        sl = sl == 2 ? 0 : sl + 1;
     };
     for (int t = tb; t < te; t += 2) {
         step(t, DB, DA);
