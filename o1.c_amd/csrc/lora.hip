@@ -451,9 +451,12 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
         // the MFMAs of tile t; the next tile's down slice is split into the
         // other plane buffer in between (independent VALU and LDS work)
         const int b = t & 1;
-        f32x16_t acc;
+        // three accumulators by part-product order (2^-16: a2b0 a1b1 a0b2;
+        // 2^-8: a1b0 a0b1; leading: a0b0), summed smallest first at the end:
+        // three dependent MFMA chains of at most 12 instead of one of 24
+        f32x16_t acc_s, acc_m, acc_l;
 #pragma unroll
-        for (int e = 0; e < 16; e++) acc[e] = 0.f;
+        for (int e = 0; e < 16; e++) acc_s[e] = acc_m[e] = acc_l[e] = 0.f;
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             const int rc = ks * 16 + lh * 8;
@@ -463,14 +466,17 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
                 a[p] = *(const bf16x8_t *)(dpl[b][p] + (kblk * 32 + l32) * LT_LD + rc);
                 bb[p] = *(const bf16x8_t *)(upl[p] + (nblk * 32 + l32) * LT_LD + rc);
             }
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], bb[0], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], bb[1], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], bb[2], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], bb[0], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], bb[1], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], bb[0], acc, 0, 0, 0);
+            acc_s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], bb[0], acc_s, 0, 0, 0);
+            acc_m = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], bb[0], acc_m, 0, 0, 0);
+            acc_l = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], bb[0], acc_l, 0, 0, 0);
+            acc_s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], bb[1], acc_s, 0, 0, 0);
+            acc_m = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], bb[1], acc_m, 0, 0, 0);
+            acc_s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], bb[2], acc_s, 0, 0, 0);
             if (ks == 1) put_down(dsplit, b ^ 1);
         }
+        f32x16_t acc;
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[e] = acc_l[e] + (acc_m[e] + acc_s[e]);
         // loads for two tiles ahead, issued after down(t+1)'s registers are
         // consumed so that waiting for those never waits for these
         const int sl2 = sl == 0 ? 2 : sl - 1;   // tile t+2 takes the slot tile t-1 used
