@@ -86,8 +86,9 @@ hd_status hd_lora_merge_gpu(hd_lora_entry *entries, size_t count, void *stream);
  * products; the delta agrees with an fp32 SGEMM up to summation order),
  * else family 1; 1 = the fp32 matrix-core kernel (v_mfma_f32_32x32x2_f32),
  * rank loop unrolled; 2 = the same, rolled (identical results to 1);
- * 3 = the split-operand product in one block per tile (identical results
- * to 0). Returns the previous setting. */
+ * 3 = the split-operand product in one block per tile (the same part
+ * products, one accumulator: equal to 0 up to fp32 summation order).
+ * Returns the previous setting. */
 int hd_lora_set_family(int family);
 
 #ifdef __cplusplus

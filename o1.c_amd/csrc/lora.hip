@@ -296,8 +296,8 @@ __global__ __launch_bounds__(256, OCC) void lora_merge_split_kernel(uint16_t *__
 //    ahead, into a ring of three 16 KB slots; the update reads W from LDS in
 //    the accumulator layout, writes the bf16 result back in place, and the
 //    tile leaves with coalesced 16-byte buffer stores;
-//  - the rank product is the split-operand form of lora_merge_split_kernel
-//    (six bf16 part products per fp32 product); the up strip's part planes
+//  - the rank product uses the part products of lora_merge_split_kernel
+//    (six bf16 part products per fp32 product, here in three accumulators); the up strip's part planes
 //    are staged once per row strip, the down slice's once per tile, into one
 //    of two plane buffers, from registers loaded a tile ahead, while the
 //    previous tile's MFMAs run (two barriers per tile);
@@ -334,14 +334,19 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
     const uint32_t OOB = 0x80000000u;
     const __amdgpu_buffer_rsrc_t rw = lt_rsrc(w, (uint32_t)((size_t)N * K * 2));
     const __amdgpu_buffer_rsrc_t ru = lt_rsrc(up, (uint32_t)((size_t)N * R * 4));
-    // W chunk i (0, 1) of this lane in a tile: LDS slot s = (2 wave + i) 64 +
-    // lane holds 16-byte chunk c = (s % 8) ^ swz(n) of tile row n = s / 8
+    // Each wave owns the 32 x 32 sub-tile of W its accumulator covers (rows
+    // nblk*32.., columns kblk*32..) and alone loads, updates and stores it,
+    // so W needs no barrier. Its 2 KB in a ring slot: instruction i, lane L
+    // -> sub-tile row r = 16 i + L / 4, 16-byte position p = L % 4 of the
+    // 64-byte row, holding column chunk c = p ^ ((r >> 2) & 3) (the XOR
+    // spreads the update's 8-byte reads of 32 rows over the banks).
+    const int kblk = wave & 1, nblk = wave >> 1;
     int wn[2], wc[2];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-        const int s = (wave * 2 + i) * 64 + lane;
-        wn[i] = s >> 3;
-        wc[i] = ((s & 7) ^ ((wn[i] >> 1) & 7)) * 8;
+        const int r = i * 16 + (lane >> 2);
+        wn[i] = nblk * 32 + r;
+        wc[i] = kblk * 32 + ((lane & 3) ^ ((r >> 2) & 3)) * 8;
     }
     // tile coordinates (row strip, column tile) and ring slots advance
     // incrementally: a division by the runtime ntk costs tens of scalar
@@ -364,11 +369,11 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
         return c.ok && gn < N && gk < K ? (uint32_t)(gn * K + gk) * 2u : OOB;
     };
     auto issue_w = [&](const TC &c, int sl) {
-        uint16_t *slot = wring[sl];
+        uint16_t *sub = wring[sl] + wave * 1024;
 #pragma unroll
         for (int i = 0; i < 2; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (HD_LDS void *)(slot + (wave * 2 + i) * 512), 16,
-                                                     w_off(c, i), 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (HD_LDS void *)(sub + i * 512), 16, w_off(c, i), 0, 0,
+                                                     0);
     };
     // down slice of a tile: ranks rr, rr + 1, columns kc .. kc + 3
     const __amdgpu_buffer_rsrc_t rd = lt_rsrc(down, (uint32_t)((size_t)R * K * 4));
@@ -419,7 +424,6 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
                 *(u32x4_t *)(upl[pl] + row * LT_LD + r16 + q * 8) = v;
             }
     };
-    const int kblk = wave & 1, nblk = wave >> 1;
     // prologue: W(tb), down(tb), W(tb+1), down(tb+1); the planes of tile tb
     TC c0 = {tb / ntk, tb % ntk, true};   // tile t
     TC c1 = tc_next(c0, tb + 1);          // tile t + 1
@@ -437,12 +441,9 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
     // tiles per trip with the two register sets swapped, so no register
     // holding a load in flight is ever copied
     auto step = [&](int t, const f32x4_t (&dsplit)[2], f32x4_t (&dload)[2]) {
-        // W(t) landed for every wave (newer than W(t): down(t), the stores of
-        // t-2, W(t+1), down(t+1), the stores of t-1 - ten operations, or a
-        // full drain since); the planes of tile t are written; every wave is
-        // past the previous tile's store pass (its ring slot is free) and
-        // MFMAs (the other plane buffer is free)
-        asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        // the planes of tile t are written; every wave is past the previous
+        // tile's MFMAs (the other plane buffer is free)
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (c0.tn != staged_tn) {
             stage_up(c0.tn);
             staged_tn = c0.tn;
@@ -482,21 +483,22 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
         const int sl2 = sl == 0 ? 2 : sl - 1;   // tile t+2 takes the slot tile t-1 used
         issue_w(c2, sl2);
         load_down(c2, dload);
-        // W update in LDS: row n = nblk*32 + l32, columns kblk*32 + 8q + 4lh .. +3.
-        // The ring is touched through assembly only: the compiler would
-        // otherwise wait for every buffer->LDS load in flight (vmcnt(0))
-        // before each access, draining the prefetch; the waits above order
-        // these accesses instead.
-        uint16_t *slot = wring[sl];
+        // W update in LDS, in this wave's own sub-tile: row l32, columns
+        // 8q + 4lh .. +3 (chunk q at position q ^ ((l32 >> 2) & 3)). W(t) of
+        // this wave landed: newer than it are down(t), the stores of t-2,
+        // W(t+1), down(t+1), the stores of t-1, W(t+2) and down(t+2) (14; on
+        // the first tiles a full drain came since). The ring is touched
+        // through assembly only: the compiler would otherwise wait for every
+        // buffer->LDS load in flight (vmcnt(0)) before each access.
+        const uint16_t *sub = wring[sl] + wave * 1024;
         {
-            const int n = nblk * 32 + l32;
             uint32_t ad[4];
 #pragma unroll
             for (int q = 0; q < 4; q++)
-                ad[q] = (uint32_t)(size_t)(HD_LDS void *)(slot + n * LT_K + (((kblk * 4 + q) ^ ((n >> 1) & 7)) * 8) +
-                                                          lh * 4);
+                ad[q] = (uint32_t)(size_t)(HD_LDS void *)(sub + (l32 * 4 + (q ^ ((l32 >> 2) & 3))) * 8 + lh * 4);
             u32x2_t wv[4];
             asm volatile(
+                "s_waitcnt vmcnt(12)\n\t"
                 "ds_read_b64 %0, %4\n\tds_read_b64 %1, %5\n\tds_read_b64 %2, %6\n\tds_read_b64 %3, %7\n\t"
                 "s_waitcnt lgkmcnt(0)"
                 : "=v"(wv[0]), "=v"(wv[1]), "=v"(wv[2]), "=v"(wv[3])
@@ -515,13 +517,12 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
                 : "v"(ad[0]), "v"(o[0]), "v"(ad[1]), "v"(o[1]), "v"(ad[2]), "v"(o[2]), "v"(ad[3]), "v"(o[3])
                 : "memory");
         }
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        // the tile leaves in the chunk order it arrived in
+        // the sub-tile leaves as it arrived (same lanes, same offsets)
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const uint32_t sa = (uint32_t)(size_t)(HD_LDS void *)(slot + ((wave * 2 + i) * 64 + lane) * 8);
+            const uint32_t sa = (uint32_t)(size_t)(HD_LDS void *)(sub + (i * 64 + lane) * 8);
             u32x4_t v;
-            asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(sa) : "memory");
+            asm volatile("s_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(sa) : "memory");
             __builtin_amdgcn_raw_buffer_store_b128(v, rw, w_off(c0, i), 0, 0);
         }
         c0 = c1;

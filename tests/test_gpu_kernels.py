@@ -658,11 +658,12 @@ def test_patchify_bf16_and_rotary_scalar_path(pkg, lib, dev):
 def test_lora_merge_families(pkg, lib, dev, N, K, R):
     """The merge kernels against each other and the fp32 oracle: the
     streaming split-operand kernel (default for rank <= 64, rank % 4 == 0)
-    equals its one-tile-per-block form bit for bit (same products, same
-    summation order), including ragged tiles and row strips that cross the
-    persistent blocks' ranges; ranks it does not take (37, 128) run the fp32
-    matrix-core kernel under the default family. Every family stays within
-    one bf16 step of the oracle (lora_merge.cu:35-104)."""
+    agrees with its one-tile-per-block form (same part products, summed in
+    three accumulators instead of one) on all but a few weights, including
+    ragged tiles and row strips that cross the persistent blocks' ranges;
+    ranks it does not take (37, 128) run the fp32 matrix-core kernel under
+    the default family, bit for bit. Every family stays within one bf16
+    step of the oracle (lora_merge.cu:35-104)."""
     rng = np.random.default_rng(N * 7 + K + R)
     w = orc.bf16_round(rng.standard_normal((N, K)).astype(np.float32) * 0.02)
     up = (rng.standard_normal((N, R)) * 0.01).astype(np.float32)
@@ -687,7 +688,7 @@ def test_lora_merge_families(pkg, lib, dev, N, K, R):
         assert close_bf16(got, ref, ulps=1, atol_rel=1e-4), fam
         assert np.mean(got == ref) > 0.999, fam
     if R <= 64 and R % 4 == 0:
-        assert np.array_equal(outs[0], outs[3])
+        assert np.mean(outs[0] == outs[3]) > 0.9999
     else:
         assert np.array_equal(outs[0], outs[1])
 
