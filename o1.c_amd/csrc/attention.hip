@@ -312,14 +312,27 @@ __global__ __launch_bounds__(NWV * 64, 8 / NWV) void flash_fwd_kernel(FaArgs a) 
         dst = a.out + (((size_t)b * a.out_rows + my_q) * a.Hq + hq) * FA_D;
     else
         dst = a.out + (((size_t)b * a.Hq + hq) * a.out_rows + my_q) * FA_D;
+    // Lanes l and l + 32 hold the low and high 4 columns of each 8-column
+    // chunk of row l. For each pair of chunks (g0, g1) one swap across the
+    // half-waves gives lane l all of chunk g0 and lane l + 32 all of g1, so
+    // each lane writes 16-byte chunks (8 stores of 16 bytes, not 16 of 8).
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-        for (int gq = 0; gq < 4; gq++) {
-            const int d = dt * 32 + gq * 8 + h * 4;
-            u32x2_t v = {pack_bf2(o[dt][gq * 4] * inv, o[dt][gq * 4 + 1] * inv),
-                         pack_bf2(o[dt][gq * 4 + 2] * inv, o[dt][gq * 4 + 3] * inv)};
-            *(u32x2_t *)(dst + d) = v;
+        for (int gp = 0; gp < 2; gp++) {
+            const int g0 = 2 * gp, g1 = g0 + 1;
+            const u32x2_t p0 = {pack_bf2(o[dt][g0 * 4] * inv, o[dt][g0 * 4 + 1] * inv),
+                                pack_bf2(o[dt][g0 * 4 + 2] * inv, o[dt][g0 * 4 + 3] * inv)};
+            const u32x2_t p1 = {pack_bf2(o[dt][g1 * 4] * inv, o[dt][g1 * 4 + 1] * inv),
+                                pack_bf2(o[dt][g1 * 4 + 2] * inv, o[dt][g1 * 4 + 3] * inv)};
+            // the half this lane gives away: chunk g1's low half (lane l) or
+            // chunk g0's high half (lane l + 32)
+            const uint32_t z0 = h ? p0[0] : p1[0], z1 = h ? p0[1] : p1[1];
+            const auto s0 = __builtin_amdgcn_permlane32_swap(z0, z0, false, false);
+            const auto s1 = __builtin_amdgcn_permlane32_swap(z1, z1, false, false);
+            const uint32_t r0 = h ? s0[0] : s0[1], r1 = h ? s1[0] : s1[1];
+            const u32x4_t v = h ? (u32x4_t){r0, r1, p1[0], p1[1]} : (u32x4_t){p0[0], p0[1], r0, r1};
+            *(u32x4_t *)(dst + dt * 32 + (h ? g1 : g0) * 8) = v;
         }
 }
 
