@@ -912,6 +912,20 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
         if (acc[0][0][0] == 12345.f) g.C[threadIdx.x] = 1;   // keeps the K loop live
         return;
     }
+    // residual epilogue: this lane's residual chunks are requested before
+    // the staging, so their latency hides under it (the write-out below
+    // then finds them in registers instead of waiting on each row group)
+    constexpr int RES_N = EPI == EPI_RES ? WTM / (64 / (C::WTN_OUT / 8)) : 1;
+    u32x4_t resv[RES_N];
+    if constexpr (EPI == EPI_RES) {
+        constexpr int CPRO_ = C::WTN_OUT / 8, RPIO_ = 64 / CPRO_;
+        const int gm0_ = m0 + wm * WTM, gn0_ = tn * C::BN_OUT + wn * C::WTN_OUT;
+#pragma unroll
+        for (int t = 0; t < RES_N; t++) {
+            const int m = gm0_ + t * RPIO_ + lane / CPRO_, n = gn0_ + (lane % CPRO_) * 8;
+            if (m < g.M && n < g.N) resv[t] = *(const u32x4_t *)(g.res + (size_t)m * g.ldc + n);
+        }
+    }
     __syncthreads();   // every wave is done with the ring before staging reuses it
 
     // QKV with 64-wide wave tiles (8 waves): the two waves of one 128-wide
@@ -963,15 +977,14 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
         qkv_epilogue<WTM, LDW>(g, stg, gm0, gn0 / 128, lane);
         return;
     }
-#pragma unroll 4
+#pragma unroll(EPI == EPI_RES ? WTM / RPIO : 4)
     for (int r0 = 0; r0 < WTM; r0 += RPIO) {
         const int r = r0 + lane / CPRO, cc = (lane % CPRO) * 8;
         const int m = gm0 + r, n = gn0 + cc;
         if (m < g.M && n < g.N) {
             u32x4_t v = *(const u32x4_t *)(stg + r * LDW + cc);
             if (EPI == EPI_BIAS || EPI == EPI_RES) {
-                u32x4_t o = EPI == EPI_BIAS ? *(const u32x4_t *)(g.bias + n)
-                                            : *(const u32x4_t *)(g.res + (size_t)m * g.ldc + n);
+                u32x4_t o = EPI == EPI_BIAS ? *(const u32x4_t *)(g.bias + n) : resv[EPI == EPI_RES ? r0 / RPIO : 0];
 #pragma unroll
                 for (int e = 0; e < 4; e++)
                     v[e] = pack_bf2(lo_bf(v[e]) + lo_bf(o[e]), hi_bf(v[e]) + hi_bf(o[e]));
