@@ -83,10 +83,11 @@ int hd_flash_attention_ws(const void *q, const void *k, const void *vt, const vo
                           int ar_len, float scale, int out_seq_major, void *ws, int64_t ws_bytes);
 /* Extension (tuning): flash kernel family. 1 = blocks of 4 waves (128
  * queries, two blocks per CU); 2 = blocks of 8 waves (256 queries, one block
- * per CU, one copy of each K / V^T tile for all of them); 0 (default) =
- * automatic: 8 waves with a tail-split workspace, full attention and
- * S >= 1024, else 4. All compute identical values. Returns the previous
- * value. */
+ * per CU, one copy of each K / V^T tile for all of them) in lockstep; 3 = the
+ * 8-wave blocks as a ping-pong (the two waves of each SIMD alternate MFMA and
+ * softmax phases, one phase apart); 0 (default) = automatic: family 3 with a
+ * tail-split workspace, full attention and S >= 1024, else 1. All compute
+ * identical values. Returns the previous value. */
 int hd_flash_set_family(int family);
 /* Workspace bytes for the tail split on the current device (one round of
  * resident flash blocks x 128 rows x (128 + 2) floats). */

@@ -554,14 +554,18 @@ def test_swiglu_tail_split(pkg, lib, dev):
     assert float(d.norm() / a.norm()) < 1e-3
 
 
-@pytest.mark.parametrize("S,ar_len,dense", [(2176, 0, False), (1152, 127, False), (1000, 0, False),
-                                            (576, 0, True)])
-def test_flash_families_identical(pkg, lib, dev, S, ar_len, dense):
-    """4-wave blocks (128 queries) and 8-wave blocks (256 queries sharing one
-    copy of each K / V^T tile) run the same per-row arithmetic: full
-    attention, a causal text prefix, S % 64 != 0 and a dense additive mask
-    agree bit for bit."""
-    B, Hq, Hkv, D = 2, 8, 2, 128
+@pytest.mark.parametrize("S,ar_len,dense,heads,use_ws", [(2176, 0, False, 8, False), (1152, 127, False, 8, False),
+                                                         (1000, 0, False, 8, False), (576, 0, True, 8, False),
+                                                         (2176, 0, False, 32, True), (1000, 0, False, 32, True),
+                                                         (640, 300, False, 32, True)])
+def test_flash_families_identical(pkg, lib, dev, S, ar_len, dense, heads, use_ws):
+    """4-wave blocks (128 queries), 8-wave blocks (256 queries sharing one
+    copy of each K / V^T tile) in lockstep and the 8-wave ping-pong blocks
+    run the same per-row arithmetic: full attention, a causal text prefix,
+    S % 64 != 0 and a dense additive mask agree bit for bit; with the
+    workspace (32 heads: the tail split runs key chunks of the last round)
+    the 8-wave families agree bit for bit too."""
+    B, Hq, Hkv, D = 2, heads, heads // 4, 128
     g = torch.Generator(device=dev).manual_seed(S + ar_len)
     q = torch.randn(B, Hq, S, D, generator=g, device=dev).to(torch.bfloat16)
     k = torch.randn(B, Hkv, S, D, generator=g, device=dev).to(torch.bfloat16)
@@ -571,20 +575,31 @@ def test_flash_families_identical(pkg, lib, dev, S, ar_len, dense):
     mask = None
     if dense:
         mask = (torch.randn(S, S, generator=g, device=dev) * 2).to(torch.bfloat16)
+    ws = torch.empty(lib.hd_flash_ws_bytes(), dtype=torch.uint8, device=dev) if use_ws else None
+    # the tail split's key chunks depend on the block size, so with the
+    # workspace only the 8-wave families (and the automatic choice where it
+    # picks them: full attention, S >= 1024) are compared
+    fams = (1, 2, 3, 0) if not use_ws else ((2, 3, 0) if ar_len == 0 and S >= 1024 else (2, 3))
     outs = []
     prev = lib.hd_flash_set_family(1)
     try:
-        for fam in (1, 2):
+        for fam in fams:
             lib.hd_flash_set_family(fam)
             o = torch.zeros(B, S, Hq * D, dtype=torch.bfloat16, device=dev)
-            assert lib.hd_flash_attention(pkg.ptr(q), pkg.ptr(k), pkg.ptr(vt),
-                                          pkg.ptr(mask) if mask is not None else None, pkg.ptr(o),
-                                          B, Hq, Hkv, S, D, ar_len, D ** -0.5, 1) == 0
+            mp = pkg.ptr(mask) if mask is not None else None
+            if use_ws:
+                rc = lib.hd_flash_attention_ws(pkg.ptr(q), pkg.ptr(k), pkg.ptr(vt), mp, pkg.ptr(o), B, Hq, Hkv, S,
+                                               D, ar_len, D ** -0.5, 1, pkg.ptr(ws), ws.numel())
+            else:
+                rc = lib.hd_flash_attention(pkg.ptr(q), pkg.ptr(k), pkg.ptr(vt), mp, pkg.ptr(o),
+                                            B, Hq, Hkv, S, D, ar_len, D ** -0.5, 1)
+            assert rc == 0
             torch.cuda.synchronize()
             outs.append(o)
     finally:
         lib.hd_flash_set_family(prev)
-    assert torch.equal(outs[0], outs[1])
+    for o in outs[1:]:
+        assert torch.equal(outs[0], o)
     assert float(outs[0].float().abs().sum(dim=-1).min()) > 0
 
 
