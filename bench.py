@@ -7,7 +7,10 @@ sequence, batch 2 (CFG cond/uncond), t-embedder MLP at t=0.5, x_embedder,
 final norm + head. Random-init bf16 weights, synthetic seeded inputs.
 A "step" = one hd_forward_batched call over both CFG sequences.
 
-Prints ONE JSON line (driver contract) with roofline and cpu_baseline.
+Prints ONE JSON line (driver contract) with roofline and cpu_baseline. The
+default run also times, on the same weights, configuration 2 (2048x2048,
+16640 tokens, batch 1) as a `c2` object and configuration 0 (one block,
+S = 1152) as a `c0` object.
 """
 import argparse
 import ctypes
@@ -60,6 +63,10 @@ def main():
                     help="with the default configuration 1, skip the configuration 2 (2048^2) timing "
                          "that the same run adds as its `c2` object")
     ap.add_argument("--c2-steps", type=int, default=10)
+    ap.add_argument("--no-c0", action="store_true",
+                    help="with the default configuration 1, skip the configuration 0 (one block, "
+                         "S = 1152) timing that the same run adds as its `c0` object")
+    ap.add_argument("--c0-steps", type=int, default=200)
     ap.add_argument("--kernel-iters", type=int, default=20)
     ap.add_argument("--flash-only", action="store_true",
                     help="run only the flash attention kernel at the configuration's shape "
@@ -176,6 +183,16 @@ def main():
                      "steps_per_s": round(1000.0 / r2["ms"], 4), "step_tflops": r2["step_tflops"],
                      "step_mfma_frac": r2["step_mfma_frac"], "wall_s": r2["wall_s"],
                      "gemm": dict(r2["gemm"], traffic=read_traffic("c2")), "attention": r2["attention"]}
+    if args.config == "c1" and not args.no_c0:
+        # configuration 0 (one block, S = 1152) on layer 0 of the same weights
+        print("[bench] configuration 0 (one block, S = 1152) on layer 0", file=sys.stderr, flush=True)
+        r0 = time_c0(pkg, lib, ctypes.byref(model.binding.blocks[0]), model.binding.blocks[0], dev,
+                     args.c0_steps, 20, args.kernel_iters)
+        res["c0"] = {"workload": CFGS["c0"]["name"], "seq_len": r0["S"], "batch": 1, "steps": args.c0_steps,
+                     "ms_per_block": round(r0["ms"], 4), "blocks_per_s": round(1000.0 / r0["ms"], 2),
+                     "block_tflops": round(r0["flops"] / (r0["ms"] * 1e-3) / 1e12, 1),
+                     "block_mfma_frac": round(r0["flops"] / (r0["ms"] * 1e-3) / PEAK_BF16, 4),
+                     "wall_s": round(r0["wall"], 3), "gemm": r0["gemm"]}
     print(json.dumps(res))
 
 
@@ -328,20 +345,17 @@ def time_config(pkg, lib, synth, model, tensors, name, steps, warmup, layers, ke
     }
 
 
-def run_c0(pkg, lib, cfg, args, dev):
-    """Configuration 0: one decoder block through hd_decoder_block_batched
-    (B = 1, S = 1152: 32x32 image tokens + 128 text tokens at position 0,
-    2-D RoPE theta 1e4), random-init bf16 weights (seed 0), N(0,1) input
-    (seed 1). A step is one block forward."""
+def time_c0(pkg, lib, block, b0, dev, steps, warmup, kernel_iters):
+    """Time configuration 0 on one decoder block's weights: the block through
+    hd_decoder_block_batched (B = 1, S = 1152: 32x32 image tokens + 128 text
+    tokens at position 0, 2-D RoPE theta 1e4) on an N(0,1) input (seed 1),
+    and the block's dominant kernel (gate/up GEMM + SwiGLU at M = 1152).
+    `block` is the ctypes reference of the block binding, `b0` the binding."""
     import numpy as np
     import torch
-    from importlib import import_module
-    synth = import_module("o1c_amd.synthetic")
+    cfg = CFGS["c0"]
     T, gh, gw = cfg["text"], cfg["gh"], cfg["gw"]
     S = T + gh * gw
-    tensors = synth.build_model(n_layers=1, seed=0, device="cuda:0")
-    model = synth.Model(tensors, 1)
-    pkg.set_block_config(theta=1e4)
     pos = np.zeros((3, S), np.float32)
     one = (ctypes.c_int * 1)
     assert lib.hd_seq_grid_positions(T, 1, one(gh), one(gw), one(0), None, 0.0, pkg.np_ptr(pos)) == S
@@ -350,42 +364,57 @@ def run_c0(pkg, lib, cfg, args, dev):
     out = torch.empty_like(x)
     sb = lib.hd_decoder_block_batched_scratch_bytes(1, S, NH, NKV, HID, FF, D)
     scr = torch.empty(sb, dtype=torch.uint8, device=dev)
-    blk = ctypes.byref(model.binding.blocks[0])
 
     def step():
-        st = lib.hd_decoder_block_batched(pkg.ptr(x), pkg.ptr(cs), None, 0, blk, pkg.ptr(scr), sb, None,
+        st = lib.hd_decoder_block_batched(pkg.ptr(x), pkg.ptr(cs), None, 0, block, pkg.ptr(scr), sb, None,
                                           pkg.ptr(out), 1, S, NH, NKV, HID, FF, D)
         if st != 0:
             raise RuntimeError(lib.hd_last_error().decode())
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms = e0.elapsed_time(e1) / args.steps
+    ms = e0.elapsed_time(e1) / steps
     gemm_tok = 2 * (HID * NH * D + 2 * HID * NKV * D + NH * D * HID + 3 * HID * FF)
     flops = S * gemm_tok + 4 * S * S * NH * D
-    # dominant kernel at this shape: the gate/up GEMM + SwiGLU (M = 1152)
     xl = torch.randn(S, HID, device=dev).to(torch.bfloat16)
     sw = torch.empty(S, FF, dtype=torch.bfloat16, device=dev)
-    b0 = model.binding.blocks[0]
     for _ in range(3):
         lib.hd_linear_swiglu(pkg.ptr(xl), ctypes.c_void_p(b0.gate_proj), ctypes.c_void_p(b0.up_proj), pkg.ptr(sw), S, FF, HID)
     torch.cuda.synchronize()
     e0.record()
-    for _ in range(args.kernel_iters):
+    for _ in range(kernel_iters):
         lib.hd_linear_swiglu(pkg.ptr(xl), ctypes.c_void_p(b0.gate_proj), ctypes.c_void_p(b0.up_proj), pkg.ptr(sw), S, FF, HID)
     e1.record()
     torch.cuda.synchronize()
-    kms = e0.elapsed_time(e1) / args.kernel_iters
+    kms = e0.elapsed_time(e1) / kernel_iters
     kflop = 2.0 * S * 2 * FF * HID
+    return {"S": S, "T": T, "gh": gh, "gw": gw, "ms": ms, "wall": wall, "flops": flops,
+            "gemm": {"kernel": "gemm_bf16 gate/up + SwiGLU epilogue", "bound": "mfma",
+                     "achieved": round(kflop / (kms * 1e-3) / 1e12, 1), "peak": PEAK_BF16 / 1e12,
+                     "unit": "TFLOP/s", "frac": round(kflop / (kms * 1e-3) / PEAK_BF16, 4),
+                     "traffic": None, "launch_ms": round(kms, 4), "shape": [S, 2 * FF, HID]}}
+
+
+def run_c0(pkg, lib, cfg, args, dev):
+    """Configuration 0: one decoder block (random-init bf16 weights, seed 0).
+    A step is one block forward."""
+    from importlib import import_module
+    synth = import_module("o1c_amd.synthetic")
+    tensors = synth.build_model(n_layers=1, seed=0, device="cuda:0")
+    model = synth.Model(tensors, 1)
+    pkg.set_block_config(theta=1e4)
+    r = time_c0(pkg, lib, ctypes.byref(model.binding.blocks[0]), model.binding.blocks[0], dev, args.steps,
+                args.warmup, args.kernel_iters)
+    S, T, gh, gw, ms = r["S"], r["T"], r["gh"], r["gw"], r["ms"]
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(S, T, gh, gw, 1, 1)
@@ -401,13 +430,10 @@ def run_c0(pkg, lib, cfg, args, dev):
         "config": {"workload": cfg["name"], "batch": 1, "seq_len": S, "image_tokens": gh * gw,
                    "text_tokens": T, "layers": 1, "hidden": HID, "heads": NH, "kv_heads": NKV,
                    "ffn": FF, "parallelism": "single GPU"},
-        "step_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
-        "step_mfma_frac": round(flops / (ms * 1e-3) / PEAK_BF16, 4),
-        "wall_s": round(wall, 3),
-        "roofline": {"kernel": "gemm_bf16 gate/up + SwiGLU epilogue", "bound": "mfma",
-                     "achieved": round(kflop / (kms * 1e-3) / 1e12, 1), "peak": PEAK_BF16 / 1e12,
-                     "unit": "TFLOP/s", "frac": round(kflop / (kms * 1e-3) / PEAK_BF16, 4),
-                     "traffic": None, "launch_ms": round(kms, 4), "shape": [S, 2 * FF, HID]},
+        "step_tflops": round(r["flops"] / (ms * 1e-3) / 1e12, 1),
+        "step_mfma_frac": round(r["flops"] / (ms * 1e-3) / PEAK_BF16, 4),
+        "wall_s": round(r["wall"], 3),
+        "roofline": r["gemm"],
         "cpu_baseline": cpu,
     }
     print(json.dumps(res))
