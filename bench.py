@@ -78,6 +78,10 @@ def main():
                     help="time each HBM-bound kernel of the path (norms, rotary, QKV epilogue, "
                          "SwiGLU, residual, head permutes, sampler pointwise, patchify) at "
                          "configuration 2's sizes and print its HBM rate against 8 TB/s")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="measure, in one process, the matrix-core ceiling probe on random and "
+                         "constant operands, hipBLASLt (torch.matmul) on the gate/up shape and this "
+                         "build's gate/up GEMMs at configurations 1 and 2")
     ap.add_argument("--kernel-only", action="store_true",
                     help="run only the dominant kernel (gate/up GEMM + SwiGLU at the step's "
                          "shape) and a 1 GiB device copy, for rocprofv3 counter passes")
@@ -107,6 +111,9 @@ def main():
         return
     if args.kernel_only:
         kernel_only(pkg, lib, B * S, args.kernel_iters)
+        return
+    if args.ceilings:
+        print(json.dumps(ceilings(pkg, lib, dev)))
         return
     if args.config == "c0":
         run_c0(pkg, lib, cfg, args, dev)
@@ -607,6 +614,64 @@ def kernel_only(pkg, lib, M, iters):
     dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"kernel_only": True, "M": M, "iters": iters, "copy_bytes": 1 << 30}))
+
+
+def ceilings(pkg, lib, dev, reps=5):
+    """What the matrix cores sustain here, measured in one process: the MFMA
+    probe (8 independent 32x32x16 bf16 chains per wave, 8 waves per CU, no
+    memory traffic) on N(0,1) and on constant operands; hipBLASLt's plain
+    GEMM (torch.matmul) on the gate/up shape (M x 4096 -> 24576); this
+    build's plain GEMM and its gate/up GEMM with the SwiGLU epilogue on the
+    same shapes (M = 8704: configuration 1, M = 16640: configuration 2).
+    Best of `reps` timed groups, each on the library's stream."""
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+
+    def best(fn, n):
+        fn()
+        torch.cuda.synchronize()
+        t = []
+        for _ in range(reps):
+            e0, e1 = ev(), ev()
+            e0.record()
+            for _ in range(n):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            t.append(e0.elapsed_time(e1) / n * 1e-3)
+        return min(t)
+
+    out = {"cus": cus, "peak_pf": PEAK_BF16 / 1e15}
+    chk = torch.empty(cus * 512, dtype=torch.float32, device=dev)
+    for name, ops in (("mfma_probe_random", torch.randn(1 << 16, device=dev).to(torch.bfloat16)),
+                      ("mfma_probe_constant", torch.full((1 << 16,), 0.5, device=dev).to(torch.bfloat16))):
+        fl = [0.0]
+
+        def probe():
+            fl[0] = lib.hd_mfma_probe(pkg.ptr(ops), ops.numel(), cus, 4096, pkg.ptr(chk))
+        t = best(probe, 5)
+        out[name] = {"pf": round(fl[0] / t / 1e15, 4), "frac": round(fl[0] / t / PEAK_BF16, 4)}
+    ws = torch.empty(lib.hd_gemm_ws_bytes(), dtype=torch.uint8, device=dev)
+    for M in (8704, 16640):
+        g = torch.Generator(device=dev).manual_seed(M)
+        x = torch.randn(M, HID, generator=g, device=dev).to(torch.bfloat16)
+        w = (torch.randn(2 * FF, HID, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        y = torch.empty(M, 2 * FF, dtype=torch.bfloat16, device=dev)
+        ys = torch.empty(M, FF, dtype=torch.bfloat16, device=dev)
+        flop = 2.0 * M * 2 * FF * HID
+        res = {}
+        t = best(lambda: torch.matmul(x, w.t(), out=y), 5)
+        res["hipblaslt_plain"] = round(flop / t / 1e15, 4)
+        t = best(lambda: lib.hd_linear_ws(pkg.ptr(x), pkg.ptr(w), None, pkg.ptr(y), M, 2 * FF, HID,
+                                          pkg.ptr(ws), ws.numel()), 5)
+        res["this_build_plain"] = round(flop / t / 1e15, 4)
+        t = best(lambda: lib.hd_linear_swiglu_ws(pkg.ptr(x), pkg.ptr(w), pkg.ptr(w[FF:]), pkg.ptr(ys), M, FF,
+                                                 HID, pkg.ptr(ws), ws.numel()), 5)
+        res["this_build_swiglu"] = round(flop / t / 1e15, 4)
+        res["unit"] = "PFLOP/s"
+        out[f"gate_up_M{M}"] = res
+    return out
 
 
 def elementwise_bench(pkg, lib, iters):

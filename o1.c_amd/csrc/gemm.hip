@@ -1676,6 +1676,56 @@ extern "C" int hd_gemm_tune_run(int cfg, int epi, const void *x, const void *w0,
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
+// Matrix-core ceiling probe (diagnostic): every wave runs 8 independent
+// v_mfma_f32_32x32x16_bf16 accumulator chains over operands held in
+// registers (4 A and 4 B fragments loaded once from `ops`, rotated so that
+// consecutive MFMAs see different data), no memory traffic in the loop. One
+// block of 8 waves per CU. Random operands give the rate the chip sustains
+// under its power limit with GEMM-like data; constant operands, the issue
+// ceiling.
+__global__ __launch_bounds__(512) void mfma_probe_kernel(const uint16_t *__restrict__ ops, int n_ops,
+                                                         int iters, float *__restrict__ out) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    bf16x8_t a[4], b[4];
+#pragma unroll
+    for (int f = 0; f < 4; f++) {
+        const long fi = ((long)(blockIdx.x * 8 + wave) * 8 + f) * 64 + lane, nf = n_ops / 8;
+        a[f] = *(const bf16x8_t *)(ops + (fi % nf) * 8);
+        b[f] = *(const bf16x8_t *)(ops + ((fi + 4 * 64) % nf) * 8);
+    }
+    f32x16_t acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[j][e] = 0.f;
+    for (int it = 0; it < iters; it += 4) {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[(j + r) & 3], b[((j >> 2) + r) & 3], acc[j], 0,
+                                                                 0, 0);
+    }
+    float t = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) t += acc[j][e];
+    out[(size_t)blockIdx.x * 512 + threadIdx.x] = t;
+}
+
+// Runs the probe on `blocks` blocks (one per CU: the CU count) with `iters`
+// (a multiple of 4) MFMA rounds per chain; returns the FLOP it performs.
+extern "C" double hd_mfma_probe(const void *ops, int n_ops, int blocks, int iters, float *out) {
+    if (!ops || !out || n_ops < 4 * 4096 + 16 || blocks <= 0 || iters <= 0 || iters % 4) {
+        snprintf(hd_cuda_errbuf(), 512, "mfma_probe: bad args");
+        return 0.0;
+    }
+    mfma_probe_kernel<<<blocks, 512, 0, hd_stream()>>>((const uint16_t *)ops, n_ops, iters, out);
+    hd_check_launch("mfma_probe");
+    return (double)blocks * 8 * 8 * (double)iters * 32.0 * 32.0 * 16.0 * 2.0;
+}
+
 extern "C" const char *hd_gemm_config_name(int M, int N, int K, int epi) {
     GemmArgs g = {};
     g.M = M; g.N = N; g.K = K;
