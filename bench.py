@@ -618,8 +618,8 @@ def kernel_only(pkg, lib, M, iters):
 
 def ceilings(pkg, lib, dev, reps=5):
     """What the matrix cores sustain here, measured in one process: the MFMA
-    probe (8 independent 32x32x16 bf16 chains per wave, 8 waves per CU, no
-    memory traffic) on N(0,1) and on constant operands; hipBLASLt's plain
+    probe (8 independent 32x32x16 bf16 chains per wave, or 16 of 16x16x32,
+    8 waves per CU, no memory traffic) on N(0,1) and on constant operands; hipBLASLt's plain
     GEMM (torch.matmul) on the gate/up shape (M x 4096 -> 24576); this
     build's plain GEMM and its gate/up GEMM with the SwiGLU epilogue on the
     same shapes (M = 8704: configuration 1, M = 16640: configuration 2).
@@ -644,14 +644,16 @@ def ceilings(pkg, lib, dev, reps=5):
 
     out = {"cus": cus, "peak_pf": PEAK_BF16 / 1e15}
     chk = torch.empty(cus * 512, dtype=torch.float32, device=dev)
-    for name, ops in (("mfma_probe_random", torch.randn(1 << 16, device=dev).to(torch.bfloat16)),
-                      ("mfma_probe_constant", torch.full((1 << 16,), 0.5, device=dev).to(torch.bfloat16))):
-        fl = [0.0]
+    for name, ops in (("random", torch.randn(1 << 16, device=dev).to(torch.bfloat16)),
+                      ("constant", torch.full((1 << 16,), 0.5, device=dev).to(torch.bfloat16))):
+        for shape in (32, 16):
+            fl = [0.0]
 
-        def probe():
-            fl[0] = lib.hd_mfma_probe(pkg.ptr(ops), ops.numel(), cus, 4096, pkg.ptr(chk))
-        t = best(probe, 5)
-        out[name] = {"pf": round(fl[0] / t / 1e15, 4), "frac": round(fl[0] / t / PEAK_BF16, 4)}
+            def probe():
+                fl[0] = lib.hd_mfma_probe(pkg.ptr(ops), ops.numel(), cus, 4096, shape, pkg.ptr(chk))
+            t = best(probe, 5)
+            out[f"mfma{shape}_probe_{name}"] = {"pf": round(fl[0] / t / 1e15, 4),
+                                               "frac": round(fl[0] / t / PEAK_BF16, 4)}
     ws = torch.empty(lib.hd_gemm_ws_bytes(), dtype=torch.uint8, device=dev)
     for M in (8704, 16640):
         g = torch.Generator(device=dev).manual_seed(M)

@@ -114,11 +114,12 @@ int hd_gemm_tune_run(int cfg, int epi, const void *x, const void *w0, const void
 
 /* Extension (diagnostic, no counterpart in the reference): matrix-core
  * ceiling probe. `blocks` blocks of 8 waves each run 8 independent
- * v_mfma_f32_32x32x16_bf16 chains for `iters` rounds (a multiple of 4) over
- * bf16 operands read once from `ops` (n_ops elements, >= 16400); `out`
- * receives blocks * 512 checksums. Returns the FLOP count of the launch
- * (0 on bad arguments). */
-double hd_mfma_probe(const void *ops, int n_ops, int blocks, int iters, float *out);
+ * v_mfma_f32_32x32x16_bf16 chains (shape 32) or 16 v_mfma_f32_16x16x32_bf16
+ * chains (shape 16) for `iters` rounds of 32x32x16-equivalent work (a
+ * multiple of 4) over bf16 operands read once from `ops` (n_ops elements,
+ * >= 16400); `out` receives blocks * 512 checksums. Returns the FLOP count
+ * of the launch (0 on bad arguments). */
+double hd_mfma_probe(const void *ops, int n_ops, int blocks, int iters, int shape, float *out);
 
 /* Name of the kernel configuration hd_linear* would launch for a shape
  * (diagnostics; static string). */

@@ -462,10 +462,10 @@ template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 0
           int LDR = 0, int MF = 32>
 __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g) {
     // MF: MFMA shape, 32 (v_mfma_f32_32x32x16_bf16) or 16 (16x16x32, SGB 3 only)
-    static_assert(MF == 32 || SGB == 3, "16x16 MFMA tiles use the continuous ring");
-    static_assert((SGB != 4 && SGB != 5) || (LDR == 5 && MF == 32 && NS == 2),
-                  "split rings: buffer loads, 2+1 stages");
-    using C = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI, MF, SGB == 4 ? 1 : 0, SGB == 5 ? 1 : 0>;
+    constexpr bool SPLITR = SGB == 4 || SGB == 5 || SGB >= 8;
+    static_assert(MF == 32 || SGB == 3 || SGB == 4 || SGB >= 8, "16x16 MFMA tiles: fragment-ring schedules");
+    static_assert(!SPLITR || (LDR == 5 && NS == 2), "split rings: buffer loads, 2+1 stages");
+    using C = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI, MF, SPLITR && SGB != 5 ? 1 : 0, SGB == 5 ? 1 : 0>;
     using AccT = typename std::conditional<MF == 32, f32x16_t, f32x4_t>::type;
     constexpr int ACCN = MF == 32 ? 16 : 4;
     constexpr int WTM = C::WTM, WTN = C::WTN, TM = C::TM, TN = C::TN, CPR = C::CPR;
@@ -696,7 +696,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
         for (; kt + NS < nk; kt++) tile(kt, T_{}, T_{});
         for (; kt + 1 < nk; kt++) tile(kt, F_{}, T_{});
         tile(kt, F_{}, F_{});
-    } else if constexpr (SGB == 4 || SGB == 5) {
+    } else if constexpr (SPLITR) {
         // The fragment ring of schedule 3 with split operand rings in the
         // 160 KB of LDS: one operand three stages deep, the other two
         // (schedule 4: A deep - the activation rows, shared by fewer of an
@@ -706,23 +706,29 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
         // tile kt (both operands of tile kt+1 landed) may leave the newest
         // deep loads in flight: the deep operand gets two tiles of latency,
         // the other one.
-        constexpr bool DA = SGB == 4;
-        constexpr int KS = BK / 16, NR = TM + TN, NM = TM * TN, AI_ = C::AI, BI_ = C::BI;
+        constexpr bool DA = SGB != 5;
+        // SGB 8-10: the fragment reads / refill loads go between every SPR-th
+        // / SPV-th MFMA
+        constexpr int SPR = SGB == 8 || SGB == 9 ? 2 : 1, SPV = SGB == 8 ? 2 : (SGB >= 9 ? 4 : 1);
+        // k-steps per tile: 16 deep (32x32x16) or 32 deep (16x16x32); a lane
+        // reads 8 consecutive k of row lane % MF, chunk lane / MF of the step
+        constexpr int KS = BK / (MF == 32 ? 16 : 32), CPS = 64 / MF;
+        constexpr int NR = TM + TN, NM = TM * TN, AI_ = C::AI, BI_ = C::BI;
         constexpr int NSA = NS + (DA ? 1 : 0), NSB = NS + (DA ? 0 : 1), ASTG = BM * BK, BSTG = BN * BK;
         constexpr int ND = DA ? AI_ : BI_, NSH = DA ? BI_ : AI_;   // loads per batch: deep, shallow
         static_assert(KS % 2 == 0, "fragment slots");
         uint16_t *const Abase = smem, *const Bbase = smem + NSA * ASTG;
-        const int lr = lane % 32, lc = lane / 32, swr = ms_swz<CPR>(lr);
+        const int lr = lane % MF, lc = lane / MF, swr = ms_swz<CPR>(lr);
         bf16x8_t af[2][TM], bw[2][TN];
         auto ld = [&](int kt, int ks, int sl) {
             const uint16_t *As = Abase + (kt % NSA) * ASTG, *Bs = Bbase + (kt % NSB) * BSTG;
-            const int c = ((ks * 2 + lc) ^ swr) * 8;
+            const int c = ((ks * CPS + lc) ^ swr) * 8;
 #pragma unroll
             for (int i = 0; i < TM; i++)
-                af[sl][i] = *(const bf16x8_t *)(As + (wm * WTM + i * 32 + lr) * BK + c);
+                af[sl][i] = *(const bf16x8_t *)(As + (wm * WTM + i * MF + lr) * BK + c);
 #pragma unroll
             for (int j = 0; j < TN; j++)
-                bw[sl][j] = *(const bf16x8_t *)(Bs + (wn * WTN + j * 32 + lr) * BK + c);
+                bw[sl][j] = *(const bf16x8_t *)(Bs + (wn * WTN + j * MF + lr) * BK + c);
         };
         auto issue_a = [&](int kt) {
             uint16_t *As = Abase + (kt % NSA) * ASTG;
@@ -785,16 +791,21 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
 #pragma unroll
                 for (int i = 0; i < TM; i++)
 #pragma unroll
-                    for (int j = 0; j < TN; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[ks & 1][j], af[ks & 1][i],
-                                                                             acc[i][j], 0, 0, 0);
+                    for (int j = 0; j < TN; j++) {
+                        if constexpr (MF == 32)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[ks & 1][j], af[ks & 1][i],
+                                                                                 acc[i][j], 0, 0, 0);
+                        else
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bw[ks & 1][j], af[ks & 1][i],
+                                                                                 acc[i][j], 0, 0, 0);
+                    }
                 const int nv = last ? (RD ? ND : 0) + (RS ? NSH : 0) : 0;
                 const int nr = !last || NX ? NR : 0;
 #pragma unroll
                 for (int q = 0; q < NM; q++) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    if (q < nv) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-                    if (q < nr) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    if (q % SPV == 0 && q / SPV < nv) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                    if (q % SPR == SPR - 1 && q / SPR < nr) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 }
             }
         };
@@ -905,6 +916,21 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
                                      acc[i][j][q * 4 + 3]};
                         *(f32x4_t *)(pt + (size_t)row * BN + col) = v;
                     }
+            return;
+        }
+    } else {
+        if (chunk >= 0) {
+            // 16x16 tiles: a lane holds rows i*16 + lane%16, columns
+            // j*16 + (lane/16)*4 .. +3 (tile-local, B-row column order)
+            float *pt = g.part + (size_t)item * BM * BN;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const int row = wm * WTM + i * 16 + (lane & 15);
+                    const int col = wn * WTN + j * 16 + (lane >> 4) * 4;
+                    *(f32x4_t *)(pt + (size_t)row * BN + col) = acc[i][j];
+                }
             return;
         }
     }
@@ -1379,7 +1405,7 @@ static void launch_ms(GemmArgs &g, void *ws = nullptr, int64_t ws_bytes = 0) {
     g.ntn = (g.N + Cfg::BN_OUT - 1) / Cfg::BN_OUT;
     const long units = (long)g.ntm * g.ntn;
     int P = 1;
-    if (ws && MF == 32)
+    if (ws)
         P = tail_split_of(units, g.K / BK, (size_t)BM * BN * 4, ws_bytes,
                           EPI == EPI_QKV ? (size_t)BM * BN * 2 : 0, OCC);
     const long n_tail = P > 1 ? units % ((long)gemm_slots() * OCC) : 0;
@@ -1457,6 +1483,11 @@ static bool run_table(int cfg, GemmArgs &g) {
     case 55: launch_ms<256, 256, 64, 2, 2, 4, EPI, 3, 1, 6>(g); return true;  // diag: no epilogue
     case 56: launch_ms<256, 256, 64, 2, 2, 4, EPI, 4, 1, 5>(g); return true;  // split rings (A 3, B 2)
     case 57: launch_ms<256, 256, 64, 2, 2, 4, EPI, 5, 1, 5>(g); return true;  // split rings (A 2, B 3)
+    case 68: launch_ms<256, 256, 64, 2, 2, 4, EPI, 4, 1, 5, 16>(g); return true;  // split rings, 16x16x32
+    case 69: launch_ms<256, 256, 64, 2, 2, 4, EPI, 8, 1, 5, 16>(g); return true;  // the same, spread 2
+    case 70: launch_ms<256, 256, 64, 2, 2, 4, EPI, 9, 1, 5, 16>(g); return true;  // reads 2, loads 4
+    case 71: launch_ms<256, 256, 64, 2, 2, 4, EPI, 10, 1, 5, 16>(g); return true; // reads 1, loads 4
+    case 72: launch_ms<256, 256, 64, 2, 4, 2, EPI, 8, 1, 5, 16>(g); return true;  // 4 x 2 waves
     case 7: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 1>(g); return true;    // diag: compute only
     case 8: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 2>(g); return true;    // diag: loads only
     default: return false;
@@ -1520,27 +1551,31 @@ static const char *pick_and_launch(GemmArgs &g, bool launch, void *ws = nullptr,
         if (launch) launch_ms<128, 128, 64, 2, 2, 2, EPI, 1, 2>(g, ws, ws_bytes);
         return p128 > 1 ? "bf16_128x128x64_w2x2_occ2_split" : "bf16_128x128x64_w2x2_occ2";
     }
-    // Family 0 (production): 8 waves (2 x 4) of 128x64 with one fragment
-    // ring across the K loop and buffer loads straight to LDS (each operand
-    // under 2 GiB: 32-bit byte offsets), the A operand's LDS ring one stage
-    // deeper than B's (schedule 4); two waves per SIMD cover each other's
-    // barrier and load-issue stalls. Family 1 (the previous
-    // kernels, kept for same-process comparisons): 4 waves of 128x128 for
-    // K <= 8192, 8 interleaved waves for deeper K.
+    // Family 0 (production): 8 waves (2 x 4) of 128x64 on v_mfma_f32_16x16x32_bf16
+    // (8 x 4 accumulator tiles per wave) with one fragment ring across the K
+    // loop and buffer loads straight to LDS (each operand under 2 GiB: 32-bit
+    // byte offsets), the A operand's LDS ring one stage deeper than B's, and
+    // the next k-step's fragment reads and the refill loads placed between
+    // every other MFMA (schedule 8); two waves per SIMD cover each other's
+    // barrier and load-issue stalls. On N(0,1) data the matrix cores sustain
+    // ~14 % more FLOP/s with 16x16x32 than with 32x32x16 instructions under
+    // the power limit. Family 2: the same MFMA tiles with equal-depth operand
+    // rings (schedule 3; the same K order, bit-identical). Family 1: the
+    // previous production kernels on v_mfma_f32_32x32x16_bf16 (kept for
+    // same-process comparisons).
     const bool fits = (size_t)(g.M + 256) * g.K * 2 < ((size_t)1 << 31) &&
                       (size_t)g.N * g.K * 2 < ((size_t)1 << 31);
     const bool use192 = c192 < c256;
     const bool split256 = p256 > 1;
     if (g_family == 2 && fits) {
-        // the production family with equal-depth operand rings (schedule 3)
         if (use192) {
-            if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 3, 1, 5>(g, ws, ws_bytes);
-            return "bf16_192x256x64_w2x4_ring_buf_s3";
+            if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 3, 1, 5, 16>(g, ws, ws_bytes);
+            return "bf16_192x256x64_w2x4_m16_ring_buf_s3";
         }
-        if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 3, 1, 5>(g, ws, ws_bytes);
-        return "bf16_256x256x64_w2x4_ring_buf_s3";
+        if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 3, 1, 5, 16>(g, ws, ws_bytes);
+        return "bf16_256x256x64_w2x4_m16_ring_buf_s3";
     }
-    if (g_family != 1) {
+    if (g_family == 1) {
         if (use192) {
             if (fits) {
                 if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 4, 1, 5>(g, ws, ws_bytes);
@@ -1556,29 +1591,20 @@ static const char *pick_and_launch(GemmArgs &g, bool launch, void *ws = nullptr,
         if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 3>(g, ws, ws_bytes);
         return split256 ? "bf16_256x256x64_w2x4_ring_tailsplit" : "bf16_256x256x64_w2x4_ring";
     }
-    const bool ring4 = g.K <= 8192 && fits;
     if (use192) {
-        if (ring4) {
-            if (launch) launch_ms<192, 256, 64, 2, 2, 2, EPI, 3, 1, 5>(g, ws, ws_bytes);
-            return "bf16_192x256x64_w2x2_ring_buf";
-        }
         if (fits) {
-            if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 1, 1, 5>(g, ws, ws_bytes);
-            return "bf16_192x256x64_w2x4_ilv_buf";
+            if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 8, 1, 5, 16>(g, ws, ws_bytes);
+            return "bf16_192x256x64_w2x4_m16_ring_buf";
         }
-        if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 1>(g, ws, ws_bytes);
-        return "bf16_192x256x64_w2x4_ilv";
-    }
-    if (ring4) {
-        if (launch) launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 5>(g, ws, ws_bytes);
-        return split256 ? "bf16_256x256x64_w2x2_ring_buf_tailsplit" : "bf16_256x256x64_w2x2_ring_buf";
+        if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 3, 1, 0, 16>(g, ws, ws_bytes);
+        return "bf16_192x256x64_w2x4_m16_ring";
     }
     if (fits) {
-        if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 1, 1, 5>(g, ws, ws_bytes);
-        return split256 ? "bf16_256x256x64_w2x4_ilv_buf_tailsplit" : "bf16_256x256x64_w2x4_ilv_buf";
+        if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 8, 1, 5, 16>(g, ws, ws_bytes);
+        return split256 ? "bf16_256x256x64_w2x4_m16_ring_buf_tailsplit" : "bf16_256x256x64_w2x4_m16_ring_buf";
     }
-    if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 1>(g, ws, ws_bytes);
-    return split256 ? "bf16_256x256x64_w2x4_ilv_tailsplit" : "bf16_256x256x64_w2x4_ilv";
+    if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 3, 1, 0, 16>(g, ws, ws_bytes);
+    return split256 ? "bf16_256x256x64_w2x4_m16_ring_tailsplit" : "bf16_256x256x64_w2x4_m16_ring";
 }
 
 static bool mfma_ok(const void *x, const void *y, int N, int K) {
@@ -1634,14 +1660,14 @@ extern "C" int hd_linear_qkv_rope_ws(const void *x, const void *wq, const void *
     const bool split256 =
         ws && tail_split_of(t256, hidden / 64, (size_t)256 * 256 * 4, ws_bytes, (size_t)256 * 256 * 2) > 1;
     const bool use192 = !split256 && quant_eff(t192) > quant_eff(t256) * 1.12;
-    if (g_family != 1) {   // 8 waves: two 64-wide wave tiles per head
+    if (g_family != 1) {   // 8 waves: two 64-wide wave tiles per head, 16x16x32 MFMA tiles
         if (g_family == 2) {
-            if (use192) launch_ms<192, 256, 64, 2, 2, 4, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
-            else launch_ms<256, 256, 64, 2, 2, 4, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
+            if (use192) launch_ms<192, 256, 64, 2, 2, 4, EPI_QKV, 3, 1, 5, 16>(g, ws, ws ? ws_bytes : 0);
+            else launch_ms<256, 256, 64, 2, 2, 4, EPI_QKV, 3, 1, 5, 16>(g, ws, ws ? ws_bytes : 0);
         } else if (use192) {
-            launch_ms<192, 256, 64, 2, 2, 4, EPI_QKV, 4, 1, 5>(g, ws, ws ? ws_bytes : 0);
+            launch_ms<192, 256, 64, 2, 2, 4, EPI_QKV, 8, 1, 5, 16>(g, ws, ws ? ws_bytes : 0);
         } else {
-            launch_ms<256, 256, 64, 2, 2, 4, EPI_QKV, 4, 1, 5>(g, ws, ws ? ws_bytes : 0);
+            launch_ms<256, 256, 64, 2, 2, 4, EPI_QKV, 8, 1, 5, 16>(g, ws, ws ? ws_bytes : 0);
         }
     } else {
         if (use192) launch_ms<192, 256, 64, 2, 2, 2, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
@@ -1677,12 +1703,14 @@ extern "C" int hd_gemm_tune_run(int cfg, int epi, const void *x, const void *w0,
 }
 
 // Matrix-core ceiling probe (diagnostic): every wave runs 8 independent
-// v_mfma_f32_32x32x16_bf16 accumulator chains over operands held in
-// registers (4 A and 4 B fragments loaded once from `ops`, rotated so that
-// consecutive MFMAs see different data), no memory traffic in the loop. One
-// block of 8 waves per CU. Random operands give the rate the chip sustains
-// under its power limit with GEMM-like data; constant operands, the issue
-// ceiling.
+// v_mfma_f32_32x32x16_bf16 accumulator chains (MF 32), or 16 chains of
+// v_mfma_f32_16x16x32_bf16 (MF 16: the same FLOP per round), over operands
+// held in registers (4 A and 4 B fragments loaded once from `ops`, rotated so
+// that consecutive MFMAs see different data), no memory traffic in the loop.
+// One block of 8 waves per CU. Random operands give the rate the chip
+// sustains under its power limit with GEMM-like data; constant operands, the
+// issue ceiling.
+template <int MF>
 __global__ __launch_bounds__(512) void mfma_probe_kernel(const uint16_t *__restrict__ ops, int n_ops,
                                                          int iters, float *__restrict__ out) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1693,37 +1721,63 @@ __global__ __launch_bounds__(512) void mfma_probe_kernel(const uint16_t *__restr
         a[f] = *(const bf16x8_t *)(ops + (fi % nf) * 8);
         b[f] = *(const bf16x8_t *)(ops + ((fi + 4 * 64) % nf) * 8);
     }
-    f32x16_t acc[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) acc[j][e] = 0.f;
-    for (int it = 0; it < iters; it += 4) {
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[(j + r) & 3], b[((j >> 2) + r) & 3], acc[j], 0,
-                                                                 0, 0);
-    }
     float t = 0.f;
+    if constexpr (MF == 32) {
+        f32x16_t acc[8];
 #pragma unroll
-    for (int j = 0; j < 8; j++)
+        for (int j = 0; j < 8; j++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) t += acc[j][e];
+            for (int e = 0; e < 16; e++) acc[j][e] = 0.f;
+        for (int it = 0; it < iters; it += 4) {
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[(j + r) & 3], b[((j >> 2) + r) & 3],
+                                                                     acc[j], 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) t += acc[j][e];
+    } else {
+        // 16x16x32: half the FLOP per instruction, twice the instructions
+        f32x4_t acc[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[j][e] = 0.f;
+        for (int it = 0; it < iters; it += 4) {
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int j = 0; j < 16; j++)
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[(j + r) & 3], b[((j >> 2) + r) & 3],
+                                                                     acc[j], 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 16; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) t += acc[j][e];
+    }
     out[(size_t)blockIdx.x * 512 + threadIdx.x] = t;
 }
 
 // Runs the probe on `blocks` blocks (one per CU: the CU count) with `iters`
-// (a multiple of 4) MFMA rounds per chain; returns the FLOP it performs.
-extern "C" double hd_mfma_probe(const void *ops, int n_ops, int blocks, int iters, float *out) {
-    if (!ops || !out || n_ops < 4 * 4096 + 16 || blocks <= 0 || iters <= 0 || iters % 4) {
+// (a multiple of 4) rounds of 32x32x16-equivalent work per chain, on MFMA
+// shape 32 or 16; returns the FLOP it performs.
+extern "C" double hd_mfma_probe(const void *ops, int n_ops, int blocks, int iters, int shape, float *out) {
+    const bool m16 = shape == 16;
+    if (m16) iters *= 2;   // the same FLOP in half-size instructions
+    if (!ops || !out || n_ops < 4 * 4096 + 16 || blocks <= 0 || iters <= 0 || iters % 4 ||
+        (shape != 16 && shape != 32)) {
         snprintf(hd_cuda_errbuf(), 512, "mfma_probe: bad args");
         return 0.0;
     }
-    mfma_probe_kernel<<<blocks, 512, 0, hd_stream()>>>((const uint16_t *)ops, n_ops, iters, out);
+    if (m16) mfma_probe_kernel<16><<<blocks, 512, 0, hd_stream()>>>((const uint16_t *)ops, n_ops, iters, out);
+    else mfma_probe_kernel<32><<<blocks, 512, 0, hd_stream()>>>((const uint16_t *)ops, n_ops, iters, out);
     hd_check_launch("mfma_probe");
-    return (double)blocks * 8 * 8 * (double)iters * 32.0 * 32.0 * 16.0 * 2.0;
+    return (double)blocks * 8 * 8 * (double)(m16 ? iters / 2 : iters) * 32.0 * 32.0 * 16.0 * 2.0;
 }
 
 extern "C" const char *hd_gemm_config_name(int M, int N, int K, int epi) {

@@ -237,7 +237,7 @@ SIGNATURES = {
     "hd_linear_concat3": (None, [P, P, c_int, P, c_int, P, c_int, P, c_int, c_int]),
     "hd_gemm_config_name": (c_char_p, [c_int, c_int, c_int, c_int]),
     "hd_gemm_tune_run": (c_int, [c_int, c_int, P, P, P, P, c_int, c_int, c_int]),
-    "hd_mfma_probe": (ctypes.c_double, [P, c_int, c_int, c_int, P]),
+    "hd_mfma_probe": (ctypes.c_double, [P, c_int, c_int, c_int, c_int, P]),
     "hd_gemm_set_family": (c_int, [c_int]),
     "hd_flash_set_family": (c_int, [c_int]),
     "hd_tokenizer_load": (c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p]),
