@@ -345,7 +345,7 @@ def time_config(pkg, lib, synth, model, tensors, name, steps, warmup, layers, ke
                  "achieved": round(achieved, 1), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
                  "frac": round(achieved * 1e12 / PEAK_BF16, 4), "launch_ms": round(kms, 4),
                  "shape": [M, 2 * FF, HID]},
-        "attention": {"kernel": "flash_pp_kernel (8-wave ping-pong; full, GQA 32/8, D=128; tail-split workspace as in the block)",
+        "attention": {"kernel": "flash_pp16_kernel (8-wave ping-pong on 16x16x32 MFMA tiles; full, GQA 32/8, D=128; tail-split workspace as in the block)",
                       "achieved": round(attn_tf, 1), "unit": "TFLOP/s",
                       "frac": round(attn_tf * 1e12 / PEAK_BF16, 4), "launch_ms": round(ams, 4)},
         "extra": extra,

@@ -653,6 +653,337 @@ __global__ __launch_bounds__(512, 1) void flash_pp_kernel(FaArgs a) {
     if (!grp) fa_barrier();
 }
 
+// 16x16x32 form of the ping-pong kernel (the automatic 8-wave choice). The
+// same phases, barriers, LDS buffers and loads as flash_pp_kernel; each
+// wave's 32 queries are two 16-query blocks, and every product runs on
+// v_mfma_f32_16x16x32_bf16 (under the power limit the matrix cores sustain
+// more FLOP/s with it on random operands than with 32x32x16):
+//  * S^T = K Q^T: 4 MFMAs of 16 keys per tile and query block, each summing
+//    4 steps of 32 head dimensions. The K rows feeding output row i of
+//    MFMA u are key(u, i) = (u/2)*32 + (i/8)*16 + (u%2)*8 + ((i/4)%2)*4 + i%4,
+//    so a lane (query lane % 16, row group lane / 16) ends with exactly the
+//    8 keys that the V^T layout stores, for each 32-key step, in its 8 P^T
+//    operand slots (perm16 columns g*8 .. g*8+7); P feeds the second MFMA
+//    straight from the S registers, as in the 32x32 kernels;
+//  * O^T = V^T P^T: 8 MFMAs of 16 head dimensions per query block, the V^T
+//    rows of MFMA pair (w, v) ordered so that a lane holds 8 consecutive
+//    dimensions w*32 + g*8 .. +7 (one 16-byte output store);
+//  * a query's 64 scores of a tile sit in the 4 lanes lane % 16 + 16 r: the
+//    row max / sum take an xor-16 and an xor-32 lane exchange;
+//  * K rows are swizzled by key bits 0-2 and 4, V^T rows by dimension bits
+//    1, 3 and 4, so every 16-lane fragment read hits 16 distinct banks.
+__device__ __forceinline__ int fa16_kswz(int row) { return (row & 7) | (((row >> 4) & 1) << 3); }
+__device__ __forceinline__ int fa16_vswz(int row) { return ((row >> 1) & 1) | (((row >> 3) & 3) << 1); }
+__device__ __forceinline__ int fa16_key(int u, int i) {
+    return (u >> 1) * 32 + (i >> 3) * 16 + (u & 1) * 8 + ((i >> 2) & 1) * 4 + (i & 3);
+}
+// max / sum over the 4 lanes lane % 16 + 16 r (v_permlane16_swap exchanges
+// rows 0 <-> 1 and 2 <-> 3 of 16 lanes, v_permlane32_swap the two halves)
+__device__ __forceinline__ float xor16_32_max(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return xor32_max(fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
+}
+__device__ __forceinline__ float xor16_32_sum(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return xor32_sum(__uint_as_float(r[0]) + __uint_as_float(r[1]));
+}
+
+template <bool MASKED>
+__global__ __launch_bounds__(512, 1) void flash_pp16_kernel(FaArgs a) {
+    constexpr int BQ = 256, LPW = 2, NB = 4;
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[NB * (FA_BK * FA_D + FA_D * FA_BK)];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = wave >> 2;
+    const int l16 = lane & 15, g = lane >> 4;
+
+    const int nqt = (a.q_row_end - a.q_row_begin + BQ - 1) / BQ;
+    const int group = a.Hq / a.Hkv;
+    int lin = blockIdx.x, chunk = -1, item = 0;
+    if (lin >= a.n_whole) {
+        item = lin - a.n_whole;
+        chunk = item % a.split;
+        lin = a.n_whole + item / a.split;
+    } else {
+        lin = fa_xcd_remap(lin, a.n_whole);
+    }
+    const int gq = lin % group; lin /= group;
+    const int qt = lin % nqt; lin /= nqt;
+    const int hk = lin % a.Hkv;
+    const int b = lin / a.Hkv;
+    const int hq = hk * group + gq;
+
+    const int qbase = a.q_row_begin + qt * BQ;
+    const int q0 = qbase + wave * 32;
+    int my_q[2];
+    my_q[0] = q0 + l16;
+    my_q[1] = q0 + 16 + l16;
+    const bool causal_block = qbase < a.ar_len;
+    int kv_end = a.S;
+    if (causal_block) {
+        int last_row = min(qbase + BQ, a.q_row_end) - 1;
+        if (last_row < a.ar_len) kv_end = last_row + 1;
+    }
+    int t_begin = 0, t_end = (kv_end + FA_BK - 1) / FA_BK;
+    if (chunk >= 0) {
+        const int nt = t_end;
+        t_begin = chunk * nt / a.split;
+        t_end = (chunk + 1) * nt / a.split;
+    }
+
+    // Q^T operand: query block qq, head dimensions ks*32 + g*8 .. +7
+    bf16x8_t qf[2][4];
+#pragma unroll
+    for (int qq = 0; qq < 2; qq++) {
+        const uint16_t *qrow = a.q + (((size_t)b * a.Hq + hq) * a.S + min(my_q[qq], a.S - 1)) * FA_D;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) qf[qq][ks] = *(const bf16x8_t *)(qrow + ks * 32 + g * 8);
+    }
+
+    const uint16_t *kbase = a.k + ((size_t)b * a.Hkv + hk) * (size_t)a.S * FA_D;
+    const uint16_t *vbase = a.vt + ((size_t)b * a.Hkv + hk) * (size_t)FA_D * a.S_pad;
+    uint16_t *Ks0 = smem, *Vs0 = smem + NB * FA_BK * FA_D;
+    const int kbytes = a.S * FA_D * 2, vbytes = FA_D * a.S_pad * 2;
+    uint32_t k_vo[LPW], v_vo[LPW];
+#pragma unroll
+    for (int i = 0; i < LPW; i++) {
+        const int krow = (wave * LPW + i) * 4 + (lane >> 4);
+        k_vo[i] = (uint32_t)(krow * FA_D + (((lane & 15) ^ fa16_kswz(krow)) * 8)) * 2;
+        const int vrow = (wave * LPW + i) * 8 + (lane >> 3);
+        v_vo[i] = (uint32_t)(vrow * a.S_pad + (((lane & 7) ^ fa16_vswz(vrow)) * 8)) * 2;
+    }
+    auto issue = [&](int t) {
+        const int buf = t & (NB - 1);
+        uint16_t *Ks = Ks0 + buf * FA_BK * FA_D, *Vs = Vs0 + buf * FA_D * FA_BK;
+#pragma unroll
+        for (int i = 0; i < LPW; i++)
+            fa_buf_load16(kbase, kbytes, k_vo[i], (uint32_t)t * FA_BK * FA_D * 2,
+                          (HD_LDS void *)(Ks + (wave * LPW + i) * 512));
+#pragma unroll
+        for (int i = 0; i < LPW; i++)
+            fa_buf_load16(vbase, vbytes, v_vo[i], (uint32_t)t * FA_BK * 2,
+                          (HD_LDS void *)(Vs + (wave * LPW + i) * 512));
+    };
+
+    // this lane's fragment rows: K row of S-MFMA u, V^T row of O-MFMA (w, v)
+    int krow_u[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) krow_u[u] = fa16_key(u, l16);
+    const int vrow0 = (l16 >> 2) * 8 + (l16 & 3);   // + w*32 + v*4
+
+    f32x4_t o[2][8];
+#pragma unroll
+    for (int qq = 0; qq < 2; qq++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[qq][i] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    float m_run[2] = {-1e30f, -1e30f}, l_run[2] = {0.f, 0.f};
+    f32x4_t s[2][4];
+    bf16x8_t pf[2][2];
+
+    auto kfrag = [&](const uint16_t *Ks, int u, int ks) {
+        const int row = krow_u[u];
+        const int c = ((ks * 4 + g) ^ fa16_kswz(row)) * 8;
+        return *(const bf16x8_t *)(Ks + row * FA_D + c);
+    };
+    auto vfrag = [&](const uint16_t *Vs, int w, int v, int st) {
+        const int row = w * 32 + v * 4 + vrow0;
+        const int c = ((st * 4 + g) ^ fa16_vswz(row)) * 8;
+        return *(const bf16x8_t *)(Vs + row * FA_BK + c);
+    };
+    // S(t) = K(t) Q^T
+    auto qk = [&](int t) {
+        const uint16_t *Ks = Ks0 + (t & (NB - 1)) * FA_BK * FA_D;
+#pragma unroll
+        for (int qq = 0; qq < 2; qq++)
+#pragma unroll
+            for (int u = 0; u < 4; u++) s[qq][u] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const bf16x8_t kf = kfrag(Ks, u, ks);
+#pragma unroll
+                for (int qq = 0; qq < 2; qq++)
+                    s[qq][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[qq][ks], s[qq][u], 0, 0, 0);
+            }
+    };
+    // O += V^T(t) P(t)^T
+    auto pv = [&](int t) {
+        const uint16_t *Vs = Vs0 + (t & (NB - 1)) * FA_D * FA_BK;
+#pragma unroll
+        for (int st = 0; st < 2; st++)
+#pragma unroll
+            for (int x = 0; x < 8; x++) {
+                const bf16x8_t vf = vfrag(Vs, x >> 1, x & 1, st);
+#pragma unroll
+                for (int qq = 0; qq < 2; qq++)
+                    o[qq][x] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[qq][st], o[qq][x], 0, 0, 0);
+            }
+    };
+    // both products of one MFMA phase, interleaved (independent chains)
+    auto pv_qk = [&](int t) {
+        const uint16_t *Vs = Vs0 + ((t - 1) & (NB - 1)) * FA_D * FA_BK;
+        const uint16_t *Ks = Ks0 + (t & (NB - 1)) * FA_BK * FA_D;
+#pragma unroll
+        for (int qq = 0; qq < 2; qq++)
+#pragma unroll
+            for (int u = 0; u < 4; u++) s[qq][u] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int y = 0; y < 16; y++) {
+            const int st = y >> 3, x = y & 7;
+            const bf16x8_t vf = vfrag(Vs, x >> 1, x & 1, st);
+#pragma unroll
+            for (int qq = 0; qq < 2; qq++)
+                o[qq][x] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[qq][st], o[qq][x], 0, 0, 0);
+            const int ks = y >> 2, u = y & 3;
+            const bf16x8_t kf = kfrag(Ks, u, ks);
+#pragma unroll
+            for (int qq = 0; qq < 2; qq++)
+                s[qq][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[qq][ks], s[qq][u], 0, 0, 0);
+        }
+        // fragment reads run FA_PF reads ahead of the MFMAs (two MFMAs per read)
+        __builtin_amdgcn_sched_group_barrier(0x100, FA_PF, 0);
+#pragma unroll
+        for (int i = 0; i < 32 - FA_PF; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * FA_PF, 0);
+    };
+    // softmax of S(t) into P(t), with the lazy O rescale
+    auto softmax = [&](int t) {
+        const int kv0 = t * FA_BK;
+        const bool need_mask = MASKED && (a.mask != nullptr || kv0 + FA_BK > a.S ||
+                                          (q0 < a.ar_len && kv0 + FA_BK - 1 > q0));
+#pragma unroll
+        for (int qq = 0; qq < 2; qq++) {
+            float mt = -INFINITY;
+            if (need_mask) {
+                const int mq = my_q[qq];
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        float v = s[qq][u][e];
+                        const int kv = kv0 + fa16_key(u, g * 4 + e);
+                        const bool dead = kv >= a.S || (mq < a.ar_len && kv > mq);
+                        if (a.mask && !dead && mq < a.S) v += bf2f(a.mask[(size_t)mq * a.S + kv]) * a.inv_scale;
+                        if (dead) v = -INFINITY;
+                        s[qq][u][e] = v;
+                        mt = fmaxf(mt, v);
+                    }
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) mt = fmaxf(mt, s[qq][u][e]);
+            }
+            mt = xor16_32_max(mt);
+            if (__builtin_amdgcn_ballot_w64((mt - m_run[qq]) * a.scale_log2 > FA_TAU)) {
+                const float m_new = fmaxf(m_run[qq], mt);
+                const float alpha = __builtin_amdgcn_exp2f((m_run[qq] - m_new) * a.scale_log2);
+                m_run[qq] = m_new;
+                l_run[qq] *= alpha;
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) o[qq][i][e] *= alpha;
+            }
+            const float mc = -m_run[qq] * a.scale_log2;
+#pragma unroll
+            for (int st = 0; st < 2; st++) {
+                bf16x8_t p8;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float p = __builtin_amdgcn_exp2f(fmaf(s[qq][st * 2 + (e >> 2)][e & 3], a.scale_log2, mc));
+                    l_run[qq] += p;
+                    p8[e] = (__bf16)p;
+                }
+                pf[qq][st] = p8;
+            }
+        }
+    };
+    auto pin_softmax = [&]() {
+        asm volatile("" ::"v"(pf[0][0]), "v"(pf[0][1]), "v"(pf[1][0]), "v"(pf[1][1]), "v"(l_run[0]),
+                     "v"(l_run[1]));
+    };
+    auto wait_next = [&](bool issued) {
+        if (issued) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        else fa_wait_vm0();
+    };
+    {
+        float *part = a.part;
+        uint16_t *outp = a.out;
+        asm volatile("" ::"s"(part), "s"(outp));
+    }
+    // barrier sequence as in flash_pp_kernel (2T + 3 barriers per wave)
+    issue(t_begin);
+    if (t_begin + 1 < t_end) {
+        issue(t_begin + 1);
+        wait_next(true);
+    } else {
+        fa_wait_vm0();
+    }
+    fa_barrier();
+    if (grp) fa_barrier();
+    {
+        const bool ld = t_begin + 2 < t_end;
+        if (ld) issue(t_begin + 2);
+        qk(t_begin);
+        wait_next(ld);
+        fa_barrier();
+    }
+    for (int t = t_begin + 1; t < t_end; t++) {
+        softmax(t - 1);
+        pin_softmax();
+        fa_barrier();
+        const bool ld = t + 2 < t_end;
+        if (ld) issue(t + 2);
+        pv_qk(t);
+        wait_next(ld);
+        fa_barrier();
+    }
+    softmax(t_end - 1);
+    pin_softmax();
+    fa_barrier();
+    pv(t_end - 1);
+    fa_barrier();
+
+    // ---- normalise and store: a lane holds dimensions w*32 + g*8 .. +7 -----
+#pragma unroll
+    for (int qq = 0; qq < 2; qq++) {
+        const float l_tot = xor16_32_sum(l_run[qq]);
+        const int row = wave * 32 + qq * 16 + l16;
+        if (chunk >= 0) {
+            float *po = a.part + ((size_t)item * BQ + row) * FA_D;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                *(f32x4_t *)(po + w * 32 + g * 8) = o[qq][w * 2];
+                *(f32x4_t *)(po + w * 32 + g * 8 + 4) = o[qq][w * 2 + 1];
+            }
+            if (g == 0) {
+                float2 *pml = (float2 *)(a.part + (size_t)(gridDim.x - a.n_whole) * BQ * FA_D);
+                pml[(size_t)item * BQ + row] = make_float2(m_run[qq], l_tot);
+            }
+        } else if (my_q[qq] < a.q_row_end) {
+            const float inv = 1.0f / l_tot;
+            uint16_t *dst;
+            if (a.out_seq_major)
+                dst = a.out + (((size_t)b * a.out_rows + my_q[qq]) * a.Hq + hq) * FA_D;
+            else
+                dst = a.out + (((size_t)b * a.Hq + hq) * a.out_rows + my_q[qq]) * FA_D;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const f32x4_t x0 = o[qq][w * 2], x1 = o[qq][w * 2 + 1];
+                const u32x4_t v = {pack_bf2(x0[0] * inv, x0[1] * inv), pack_bf2(x0[2] * inv, x0[3] * inv),
+                                   pack_bf2(x1[0] * inv, x1[1] * inv), pack_bf2(x1[2] * inv, x1[3] * inv)};
+                *(u32x4_t *)(dst + w * 32 + g * 8) = v;
+            }
+        }
+    }
+    if (!grp) fa_barrier();
+}
+
 // V [BH, S, D] -> vt [BH, D, S_pad] with perm16 columns and zero padding.
 __global__ __launch_bounds__(256) void fa_vt_kernel(const uint16_t *v, uint16_t *vt, int S,
                                                     int S_pad) {
@@ -731,12 +1062,15 @@ static int fa_slots(int nwv = 4) {
 }
 
 // hd_flash_set_family: 0 = automatic (below), 1 = 4-wave blocks, 2 = 8-wave
-// blocks in lockstep (flash_fwd_kernel), 3 = 8-wave ping-pong blocks
-// (flash_pp_kernel, the automatic choice for 8 waves)
+// blocks in lockstep (flash_fwd_kernel), 3 = 8-wave ping-pong blocks on
+// 32x32x16 MFMA tiles (flash_pp_kernel), 4 = 8-wave ping-pong blocks on
+// 16x16x32 tiles (flash_pp16_kernel, the automatic choice for 8 waves).
+// Families 1-3 run the same per-row arithmetic (bit-identical); family 4
+// sums the same products in 32-wide instead of 16-wide groups.
 static int g_fa_family = 0;
 extern "C" int hd_flash_set_family(int family) {
     const int prev = g_fa_family;
-    g_fa_family = family >= 1 && family <= 3 ? family : 0;
+    g_fa_family = family >= 1 && family <= 4 ? family : 0;
     return prev;
 }
 
@@ -806,8 +1140,10 @@ static int fa_launch(const void *q, const void *k, const void *vt, const void *m
     // 4-wave blocks otherwise (without the split their finer grain wins)
     const bool split_ok = ws && !mask && ar_len == 0;
     const int nwv = g_fa_family == 1 ? 4 : g_fa_family >= 2 ? 8 : (split_ok && seq >= 1024 ? 8 : 4);
-    // the ping-pong form: bit-identical, +2.5-4.7 % at S = 4352-16640
+    // the ping-pong form: +2.5-4.7 % at S = 4352-16640 over the lockstep
+    // blocks; on 16x16x32 MFMA tiles unless family 3 asks for 32x32x16
     const bool pp = nwv == 8 && g_fa_family != 2;
+    const bool pp16 = pp && g_fa_family != 3;
     const int BQ = nwv * 32;
     const int nqt = (q_row_end - q_row_begin + BQ - 1) / BQ;
     const int units = batch * hq * nqt;
@@ -832,7 +1168,10 @@ static int fa_launch(const void *q, const void *k, const void *vt, const void *m
         }
     }
     dim3 grid((unsigned)(a.n_whole + n_tail * a.split));
-    if (pp) {
+    if (pp16) {
+        if (masked) flash_pp16_kernel<true><<<grid, 512, 0, st>>>(a);
+        else flash_pp16_kernel<false><<<grid, 512, 0, st>>>(a);
+    } else if (pp) {
         if (masked) flash_pp_kernel<true><<<grid, 512, 0, st>>>(a);
         else flash_pp_kernel<false><<<grid, 512, 0, st>>>(a);
     } else if (nwv == 8) {

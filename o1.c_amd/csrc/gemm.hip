@@ -465,7 +465,8 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
     constexpr bool SPLITR = SGB == 4 || SGB == 5 || SGB >= 8;
     static_assert(MF == 32 || SGB == 3 || SGB == 4 || SGB >= 8, "16x16 MFMA tiles: fragment-ring schedules");
     static_assert(!SPLITR || (LDR == 5 && NS == 2), "split rings: buffer loads, 2+1 stages");
-    using C = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI, MF, SPLITR && SGB != 5 ? 1 : 0, SGB == 5 ? 1 : 0>;
+    constexpr bool BDEEP = SGB == 5 || SGB == 11;
+    using C = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI, MF, SPLITR && !BDEEP ? 1 : 0, BDEEP ? 1 : 0>;
     using AccT = typename std::conditional<MF == 32, f32x16_t, f32x4_t>::type;
     constexpr int ACCN = MF == 32 ? 16 : 4;
     constexpr int WTM = C::WTM, WTN = C::WTN, TM = C::TM, TN = C::TN, CPR = C::CPR;
@@ -706,10 +707,11 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
         // tile kt (both operands of tile kt+1 landed) may leave the newest
         // deep loads in flight: the deep operand gets two tiles of latency,
         // the other one.
-        constexpr bool DA = SGB != 5;
+        constexpr bool DA = !BDEEP;
         // SGB 8-10: the fragment reads / refill loads go between every SPR-th
         // / SPV-th MFMA
-        constexpr int SPR = SGB == 8 || SGB == 9 ? 2 : 1, SPV = SGB == 8 ? 2 : (SGB >= 9 ? 4 : 1);
+        constexpr int SPR = SGB == 8 || SGB == 9 || SGB == 11 ? 2 : 1,
+                      SPV = SGB == 8 || SGB == 11 ? 2 : (SGB == 9 || SGB == 10 ? 4 : 1);
         // k-steps per tile: 16 deep (32x32x16) or 32 deep (16x16x32); a lane
         // reads 8 consecutive k of row lane % MF, chunk lane / MF of the step
         constexpr int KS = BK / (MF == 32 ? 16 : 32), CPS = 64 / MF;
@@ -1488,6 +1490,7 @@ static bool run_table(int cfg, GemmArgs &g) {
     case 70: launch_ms<256, 256, 64, 2, 2, 4, EPI, 9, 1, 5, 16>(g); return true;  // reads 2, loads 4
     case 71: launch_ms<256, 256, 64, 2, 2, 4, EPI, 10, 1, 5, 16>(g); return true; // reads 1, loads 4
     case 72: launch_ms<256, 256, 64, 2, 4, 2, EPI, 8, 1, 5, 16>(g); return true;  // 4 x 2 waves
+    case 73: launch_ms<256, 256, 64, 2, 2, 4, EPI, 11, 1, 5, 16>(g); return true; // B ring deep
     case 7: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 1>(g); return true;    // diag: compute only
     case 8: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 2>(g); return true;    // diag: loads only
     default: return false;
