@@ -690,6 +690,7 @@ __device__ __forceinline__ float xor16_32_sum(float v) {
 
 template <bool MASKED>
 __global__ __launch_bounds__(512, 1) void flash_pp16_kernel(FaArgs a) {
+    constexpr int PF16 = FA_PF;   // 4 and 12 measured equal or slower
     constexpr int BQ = 256, LPW = 2, NB = 4;
     __shared__ __attribute__((aligned(1024))) uint16_t smem[NB * (FA_BK * FA_D + FA_D * FA_BK)];
     const int lane = threadIdx.x & 63;
@@ -841,14 +842,14 @@ __global__ __launch_bounds__(512, 1) void flash_pp16_kernel(FaArgs a) {
             for (int qq = 0; qq < 2; qq++)
                 s[qq][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[qq][ks], s[qq][u], 0, 0, 0);
         }
-        // fragment reads run FA_PF reads ahead of the MFMAs (two MFMAs per read)
-        __builtin_amdgcn_sched_group_barrier(0x100, FA_PF, 0);
+        // fragment reads run PF16 reads ahead of the MFMAs (two MFMAs per read)
+        __builtin_amdgcn_sched_group_barrier(0x100, PF16, 0);
 #pragma unroll
-        for (int i = 0; i < 32 - FA_PF; i++) {
+        for (int i = 0; i < 32 - PF16; i++) {
             __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 2 * FA_PF, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * PF16, 0);
     };
     // softmax of S(t) into P(t), with the lazy O rescale
     auto softmax = [&](int t) {
