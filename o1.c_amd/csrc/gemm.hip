@@ -1770,8 +1770,7 @@ __global__ __launch_bounds__(512) void mfma_probe_kernel(const uint16_t *__restr
 // (a multiple of 4) rounds of 32x32x16-equivalent work per chain, on MFMA
 // shape 32 or 16; returns the FLOP it performs.
 extern "C" double hd_mfma_probe(const void *ops, int n_ops, int blocks, int iters, int shape, float *out) {
-    const bool m16 = shape == 16;
-    if (m16) iters *= 2;   // the same FLOP in half-size instructions
+    const bool m16 = shape == 16;   // 16 chains of half-size instructions: the same FLOP per round
     if (!ops || !out || n_ops < 4 * 4096 + 16 || blocks <= 0 || iters <= 0 || iters % 4 ||
         (shape != 16 && shape != 32)) {
         snprintf(hd_cuda_errbuf(), 512, "mfma_probe: bad args");
@@ -1780,7 +1779,7 @@ extern "C" double hd_mfma_probe(const void *ops, int n_ops, int blocks, int iter
     if (m16) mfma_probe_kernel<16><<<blocks, 512, 0, hd_stream()>>>((const uint16_t *)ops, n_ops, iters, out);
     else mfma_probe_kernel<32><<<blocks, 512, 0, hd_stream()>>>((const uint16_t *)ops, n_ops, iters, out);
     hd_check_launch("mfma_probe");
-    return (double)blocks * 8 * 8 * (double)(m16 ? iters / 2 : iters) * 32.0 * 32.0 * 16.0 * 2.0;
+    return (double)blocks * 8 * 8 * (double)iters * 32.0 * 32.0 * 16.0 * 2.0;
 }
 
 extern "C" const char *hd_gemm_config_name(int M, int N, int K, int epi) {
