@@ -144,11 +144,14 @@ int hd_linear_qkv_rope_ws(const void *x, const void *wq, const void *wk, const v
                           float eps, void *ws, int64_t ws_bytes);
 
 /* Diagnostics/tuning: kernel family for the production GEMMs. 0 (default):
- * 8-wave fragment-ring tiles with buffer loads for every K (the fused QKV
- * epilogue included), the A operand's LDS ring three stages deep and B's
- * two; 2: the same tiles with both rings two stages deep; 1: the previous
- * kernels, 4-wave fragment-ring tiles for K <= 8192 and 8-wave interleaved
- * tiles above. All compute identical values. Returns the previous value. */
+ * 8-wave fragment-ring tiles on v_mfma_f32_16x16x32_bf16 with buffer loads
+ * for every K (the fused QKV epilogue included), the A operand's LDS ring
+ * three stages deep and B's two; 2: the same tiles with both rings two
+ * stages deep (identical values to 0); 1: the previous kernels on
+ * v_mfma_f32_32x32x16_bf16 (the same split rings; the fused QKV epilogue on
+ * 4-wave tiles), which sum each output's K products in 16-wide instead of
+ * 32-wide groups (values within fp32 reassociation of family 0). Returns the
+ * previous value. */
 int hd_gemm_set_family(int family);
 
 #ifdef __cplusplus
