@@ -1369,6 +1369,39 @@ __global__ __launch_bounds__(64) void gemm_tail_qkv_epi_kernel(GemmArgs g, int n
 }
 
 // Resident blocks of one round (one GEMM block per CU).
+// EPI_QKV tail tiles in one pass: one wave per (tile, 64-row slice, head)
+// sums the K chunks' fp32 partials of its rows (in chunk order, as
+// gemm_tail_merge_kernel does), stages the bf16 projection in LDS exactly as
+// gemm_ms_kernel stages it and runs the same qkv_epilogue; no bf16 staging
+// round trip through memory and one launch instead of two.
+template <int BM, int BN>
+__global__ __launch_bounds__(64) void gemm_tail_qkv_fused_kernel(GemmArgs g, int n_tail) {
+    constexpr int RS = 64, LDW = 128 + 8, GROUP_M = 8, NSL = BM / RS, NH = BN / 128;
+    __shared__ __attribute__((aligned(16))) uint16_t stg[RS * LDW];
+    const int lane = threadIdx.x;
+    const int b = blockIdx.x;
+    const int hc = b % NH, sl = (b / NH) % NSL, t = b / (NH * NSL);
+    const int lin = g.n_whole + t;
+    const int in_group = GROUP_M * g.ntn;
+    const int first_m = (lin / in_group) * GROUP_M;
+    const int gm = min(g.ntm - first_m, GROUP_M);
+    const int tm = first_m + (lin % in_group) % gm, tn = (lin % in_group) / gm;
+    // lane: 4 consecutive columns c4 .. c4+3 of rows r0 + 2i (i < 32)
+    const int c4 = (lane % 32) * 4, rh = lane / 32;
+#pragma unroll 4
+    for (int i = 0; i < RS / 2; i++) {
+        const int r = 2 * i + rh;
+        f32x4_t a = {0.f, 0.f, 0.f, 0.f};
+        for (int p = 0; p < g.split; p++)
+            a += *(const f32x4_t *)(g.part + ((size_t)(t * g.split + p) * BM + sl * RS + r) * BN + hc * 128 + c4);
+        *(u32x2_t *)(stg + r * LDW + c4) = (u32x2_t){pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    qkv_epilogue<RS, LDW>(g, stg, tm * BM + sl * RS, (tn * BN) / 128 + hc, lane);
+}
+
 static int gemm_slots() {
     static int dev_cached = -1, cus = 0;
     int dev = 0;
@@ -1417,12 +1450,17 @@ static void launch_ms(GemmArgs &g, void *ws = nullptr, int64_t ws_bytes = 0) {
     gemm_ms_kernel<BM, BN, BK, NS, WGM, WGN, EPI, SGB, OCC, LDR, MF>
         <<<(unsigned)(g.n_whole + n_tail * P), Cfg::NT, 0, hd_stream()>>>(g);
     if (n_tail) {
-        gemm_tail_merge_kernel<BM, BN, WGN, EPI>
-            <<<hd_cdiv((size_t)n_tail * BM * (Cfg::BN_OUT / 4), 256), 256, 0, hd_stream()>>>(
-                g, (int)n_tail);
-        if constexpr (EPI == EPI_QKV)
-            gemm_tail_qkv_epi_kernel<BM, BN>
-                <<<(unsigned)(n_tail * (BM / 32) * (BN / 128)), 64, 0, hd_stream()>>>(g, (int)n_tail);
+        if constexpr (EPI == EPI_QKV && BM % 64 == 0) {
+            gemm_tail_qkv_fused_kernel<BM, BN>
+                <<<(unsigned)(n_tail * (BM / 64) * (BN / 128)), 64, 0, hd_stream()>>>(g, (int)n_tail);
+        } else {
+            gemm_tail_merge_kernel<BM, BN, WGN, EPI>
+                <<<hd_cdiv((size_t)n_tail * BM * (Cfg::BN_OUT / 4), 256), 256, 0, hd_stream()>>>(
+                    g, (int)n_tail);
+            if constexpr (EPI == EPI_QKV)
+                gemm_tail_qkv_epi_kernel<BM, BN>
+                    <<<(unsigned)(n_tail * (BM / 32) * (BN / 128)), 64, 0, hd_stream()>>>(g, (int)n_tail);
+        }
     }
 }
 
