@@ -227,3 +227,25 @@ def test_swiglu_epilogue_vs_exact_division(pkg, lib, dev):
     print("identical fraction", same)
     assert same >= 0.999
     assert close_bf16(a, b, ulps=1)
+
+
+@pytest.mark.parametrize("shape", [32, 16])
+def test_mfma_probe_checksums(pkg, lib, dev, shape):
+    """The matrix-core ceiling probe (diagnostic) on constant operands: every
+    lane's checksum is the closed form of its 8 (or 16) accumulator chains,
+    iters rounds of dot products of 16 (32) products of 0.5 x 0.5 per step,
+    and the returned FLOP count is blocks x 8 waves x 8 x iters x 32768;
+    bad arguments return 0."""
+    blocks, iters = 4, 8
+    ops = torch.full((1 << 16,), 0.5, device=dev).to(torch.bfloat16)
+    out = torch.zeros(blocks * 512, dtype=torch.float32, device=dev)
+    fl = lib.hd_mfma_probe(pkg.ptr(ops), ops.numel(), blocks, iters, shape, pkg.ptr(out))
+    torch.cuda.synchronize()
+    assert fl == blocks * 8 * 8 * iters * 32768
+    # each output element of one chain accumulates iters MFMAs of K products
+    # of 0.25; a lane holds 16 (32x32) or 4 (16x16) elements of 8 (16) chains
+    k, per_lane = (16, 8 * 16) if shape == 32 else (32, 16 * 4)
+    want = iters * k * 0.25 * per_lane
+    assert torch.allclose(out, torch.full_like(out, want))
+    assert lib.hd_mfma_probe(pkg.ptr(ops), ops.numel(), blocks, 6, shape, pkg.ptr(out)) == 0
+    assert lib.hd_mfma_probe(pkg.ptr(ops), ops.numel(), blocks, iters, 8, pkg.ptr(out)) == 0
