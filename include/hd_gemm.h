@@ -3,8 +3,8 @@
 
 /*
  * GEMM runtime of the MI355X engine: hand-written bf16 MFMA kernels for
- * gfx950 (v_mfma_f32_32x32x16_bf16, fp32 accumulation, LDS double-buffered
- * tiles filled by direct global->LDS loads, fused epilogues).
+ * gfx950 (v_mfma_f32_16x16x32_bf16, fp32 accumulation, multi-stage LDS
+ * rings filled by direct global->LDS loads, fused epilogues).
  *
  * Replaces the reference's src/cuda/gemm.h (lines 35-68). Same symbols and
  * argument meaning. There is no vendor library behind hd_linear: the
