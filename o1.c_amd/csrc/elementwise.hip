@@ -114,13 +114,99 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
     }
 }
 
+// The same row math for cols <= 4096 (cols % 8 == 0, 16-byte aligned rows)
+// with two rows per wave: both rows' loads are in flight together and the
+// weight chunks are read once for the pair. Halving the wave count puts a
+// whole block-sized activation (8704 rows) in one round of resident waves.
+__global__ __launch_bounds__(256) void rmsnorm2_kernel(
+    const uint16_t *__restrict__ x, const uint16_t *__restrict__ a,
+    const uint16_t *__restrict__ w, uint16_t *__restrict__ sum_out,
+    uint16_t *__restrict__ y, int rows, int cols, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 2;
+    if (row0 >= rows) return;
+    const bool two = row0 + 1 < rows;
+    const int nch = cols >> 3;
+    u32x4_t buf[2][8];
+    float ss[2] = {0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        if (q == 1 && !two) break;
+        const size_t base = (size_t)(row0 + q) * cols;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int c = lane + i * 64;
+            if (c < nch) buf[q][i] = *(const u32x4_t *)(x + base + (size_t)c * 8);
+        }
+    }
+    if (a) {
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            if (q == 1 && !two) break;
+            const size_t base = (size_t)(row0 + q) * cols;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int c = lane + i * 64;
+                if (c < nch) {
+                    const u32x4_t r = *(const u32x4_t *)(a + base + (size_t)c * 8);
+                    u32x4_t v = buf[q][i];
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        v[j] = pack_bf2(lo_bf(v[j]) + lo_bf(r[j]), hi_bf(v[j]) + hi_bf(r[j]));
+                    if (sum_out) *(u32x4_t *)(sum_out + base + (size_t)c * 8) = v;
+                    buf[q][i] = v;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        if (q == 1 && !two) break;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int c = lane + i * 64;
+            if (c < nch) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float l = lo_bf(buf[q][i][j]), h = hi_bf(buf[q][i][j]);
+                    ss[q] += l * l + h * h;
+                }
+            }
+        }
+    }
+    const float inv0 = 1.0f / sqrtf(wave_sum(ss[0]) / (float)cols + eps);
+    const float inv1 = 1.0f / sqrtf(wave_sum(ss[1]) / (float)cols + eps);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int c = lane + i * 64;
+        if (c < nch) {
+            const u32x4_t wv = *(const u32x4_t *)(w + (size_t)c * 8);
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                if (q == 1 && !two) break;
+                const float inv = q ? inv1 : inv0;
+                const u32x4_t v = buf[q][i];
+                u32x4_t o;
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    o[j] = pack_bf2(lo_bf(wv[j]) * lo_bf(v[j]) * inv, hi_bf(wv[j]) * hi_bf(v[j]) * inv);
+                *(u32x4_t *)(y + (size_t)(row0 + q) * cols + (size_t)c * 8) = o;
+            }
+        }
+    }
+}
+
 static void launch_rmsnorm(const void *x, const void *a, const void *w, void *s,
                            void *y, int rows, int cols, float eps) {
     bool vec = (cols % 8 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) &&
                ((uintptr_t)w % 16 == 0) && (!a || (uintptr_t)a % 16 == 0) &&
                (!s || (uintptr_t)s % 16 == 0) && !(a && !s && cols > 4096);
     dim3 grid(hd_cdiv(rows, 4));
-    if (vec)
+    if (vec && cols <= 4096 && rows >= 1024)
+        rmsnorm2_kernel<<<dim3(hd_cdiv(rows, 8)), 256, 0, hd_stream()>>>(
+            (const uint16_t *)x, (const uint16_t *)a, (const uint16_t *)w, (uint16_t *)s,
+            (uint16_t *)y, rows, cols, eps);
+    else if (vec)
         rmsnorm_kernel<true><<<grid, 256, 0, hd_stream()>>>(
             (const uint16_t *)x, (const uint16_t *)a, (const uint16_t *)w, (uint16_t *)s,
             (uint16_t *)y, rows, cols, eps);

@@ -247,5 +247,8 @@ def test_mfma_probe_checksums(pkg, lib, dev, shape):
     k, per_lane = (16, 8 * 16) if shape == 32 else (32, 16 * 4)
     want = iters * k * 0.25 * per_lane
     assert torch.allclose(out, torch.full_like(out, want))
-    assert lib.hd_mfma_probe(pkg.ptr(ops), ops.numel(), blocks, 6, shape, pkg.ptr(out)) == 0
-    assert lib.hd_mfma_probe(pkg.ptr(ops), ops.numel(), blocks, iters, 8, pkg.ptr(out)) == 0
+    for bad_iters, bad_shape in ((6, shape), (iters, 8)):
+        assert lib.hd_mfma_probe(pkg.ptr(ops), ops.numel(), blocks, bad_iters, bad_shape,
+                                 pkg.ptr(out)) == 0
+        with pytest.raises(RuntimeError, match="mfma_probe: bad args"):
+            pkg.check_prim("mfma_probe")   # reports through the error buffer, then clears it

@@ -19,7 +19,8 @@ def host(t):
     return t.float().cpu().numpy()
 
 
-@pytest.mark.parametrize("rows,cols", [(37, 4096), (300, 128), (5, 200), (4, 8)])
+@pytest.mark.parametrize("rows,cols", [(37, 4096), (300, 128), (5, 200), (4, 8), (1031, 4096),
+                                       (1030, 1000)])
 def test_rmsnorm(pkg, lib, dev, rows, cols):
     rng = np.random.default_rng(rows)
     x = orc.bf16_round(rng.standard_normal((rows, cols)) * 3)
@@ -30,17 +31,25 @@ def test_rmsnorm(pkg, lib, dev, rows, cols):
     pkg.check_prim("rmsnorm")
     ref = orc.rmsnorm(x, w, 1e-6, 1)
     assert close_bf16(host(y), ref, ulps=1, atol_rel=0)
+    if rows >= 1024:
+        # two-rows-per-wave kernel against the one-row kernel (40-row call)
+        y40 = torch.empty(40, cols, dtype=torch.bfloat16, device=dev)
+        lib.hd_rmsnorm(pkg.ptr(xd), pkg.ptr(wd), pkg.ptr(y40), 40, cols, 1e-6)
+        assert torch.equal(y[:40], y40)
+        lib.hd_rmsnorm(pkg.ptr(xd[-40:]), pkg.ptr(wd), pkg.ptr(y40), 40, cols, 1e-6)
+        assert torch.equal(y[-40:], y40)
 
 
-def test_add_rmsnorm(pkg, lib, dev):
+@pytest.mark.parametrize("rows", [64, 1033])
+def test_add_rmsnorm(pkg, lib, dev, rows):
     rng = np.random.default_rng(1)
-    x = orc.bf16_round(rng.standard_normal((64, 4096)))
-    a = orc.bf16_round(rng.standard_normal((64, 4096)))
+    x = orc.bf16_round(rng.standard_normal((rows, 4096)))
+    a = orc.bf16_round(rng.standard_normal((rows, 4096)))
     w = orc.bf16_round(1 + rng.standard_normal(4096) * 0.1)
-    s = torch.empty(64, 4096, dtype=torch.bfloat16, device=dev)
+    s = torch.empty(rows, 4096, dtype=torch.bfloat16, device=dev)
     y = torch.empty_like(s)
     xd, ad, wd = dbf(x, dev), dbf(a, dev), dbf(w, dev)
-    lib.hd_add_rmsnorm(pkg.ptr(xd), pkg.ptr(ad), pkg.ptr(wd), pkg.ptr(s), pkg.ptr(y), 64, 4096, 1e-6)
+    lib.hd_add_rmsnorm(pkg.ptr(xd), pkg.ptr(ad), pkg.ptr(wd), pkg.ptr(s), pkg.ptr(y), rows, 4096, 1e-6)
     pkg.check_prim("add_rmsnorm")
     sref = orc.residual_add(x, a, 1)
     assert np.array_equal(host(s), sref)
