@@ -1386,15 +1386,28 @@ __global__ __launch_bounds__(64) void gemm_tail_qkv_fused_kernel(GemmArgs g, int
     const int first_m = (lin / in_group) * GROUP_M;
     const int gm = min(g.ntm - first_m, GROUP_M);
     const int tm = first_m + (lin % in_group) % gm, tn = (lin % in_group) / gm;
-    // lane: 4 consecutive columns c4 .. c4+3 of rows r0 + 2i (i < 32)
+    // lane: 4 consecutive columns c4 .. c4+3 of rows 2i + rh (i < 32); the
+    // partials of 4 rows x every chunk (split <= 8) are loaded before any
+    // is summed, so up to 32 loads per lane are in flight
     const int c4 = (lane % 32) * 4, rh = lane / 32;
-#pragma unroll 4
-    for (int i = 0; i < RS / 2; i++) {
-        const int r = 2 * i + rh;
-        f32x4_t a = {0.f, 0.f, 0.f, 0.f};
-        for (int p = 0; p < g.split; p++)
-            a += *(const f32x4_t *)(g.part + ((size_t)(t * g.split + p) * BM + sl * RS + r) * BN + hc * 128 + c4);
-        *(u32x2_t *)(stg + r * LDW + c4) = (u32x2_t){pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
+    const float *pbase = g.part + ((size_t)t * g.split * BM + sl * RS + rh) * BN + hc * 128 + c4;
+    for (int i0 = 0; i0 < RS / 2; i0 += 4) {
+        f32x4_t pv[8][4];
+#pragma unroll
+        for (int p = 0; p < 8; p++)
+            if (p < g.split)
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    pv[p][k] = *(const f32x4_t *)(pbase + ((size_t)p * BM + 2 * (i0 + k)) * BN);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            f32x4_t a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int p = 0; p < 8; p++)
+                if (p < g.split) a += pv[p][k];
+            const int r = 2 * (i0 + k) + rh;
+            *(u32x2_t *)(stg + r * LDW + c4) = (u32x2_t){pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
+        }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
