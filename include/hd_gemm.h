@@ -150,8 +150,10 @@ int hd_linear_qkv_rope_ws(const void *x, const void *wq, const void *wk, const v
  * stages deep (identical values to 0); 1: the previous kernels on
  * v_mfma_f32_32x32x16_bf16 (the same split rings; the fused QKV epilogue on
  * 4-wave tiles), which sum each output's K products in 16-wide instead of
- * 32-wide groups (values within fp32 reassociation of family 0). Returns the
- * previous value. */
+ * 32-wide groups (values within fp32 reassociation of family 0); 3: family 0
+ * without the small-grid rule (grids of 256 x 256 tiles that fit one round,
+ * K <= 4096, no SwiGLU: 128 x 128 tiles, two blocks per CU, no K split), for
+ * comparisons. Returns the previous value. */
 int hd_gemm_set_family(int family);
 
 #ifdef __cplusplus

@@ -1542,6 +1542,9 @@ static bool run_table(int cfg, GemmArgs &g) {
     case 71: launch_ms<256, 256, 64, 2, 2, 4, EPI, 10, 1, 5, 16>(g); return true; // reads 1, loads 4
     case 72: launch_ms<256, 256, 64, 2, 4, 2, EPI, 8, 1, 5, 16>(g); return true;  // 4 x 2 waves
     case 73: launch_ms<256, 256, 64, 2, 2, 4, EPI, 11, 1, 5, 16>(g); return true; // B ring deep
+    case 74: launch_ms<128, 128, 64, 2, 2, 2, EPI, 8, 2, 5, 16>(g); return true;  // small grids, 16x16x32
+    case 75: launch_ms<128, 128, 64, 2, 2, 2, EPI, 4, 2, 5, 16>(g); return true;  // the same, no spread
+    case 76: launch_ms<128, 128, 64, 2, 2, 2, EPI, 3, 2, 5, 16>(g); return true;  // equal-depth rings
     case 7: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 1>(g); return true;    // diag: compute only
     case 8: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 2>(g); return true;    // diag: loads only
     default: return false;
@@ -1556,7 +1559,7 @@ static int g_family = 0;   // hd_gemm_set_family
 
 extern "C" int hd_gemm_set_family(int family) {
     const int prev = g_family;
-    g_family = family == 1 || family == 2 ? family : 0;
+    g_family = family >= 1 && family <= 3 ? family : 0;
     return prev;
 }
 
@@ -1601,7 +1604,26 @@ static const char *pick_and_launch(GemmArgs &g, bool launch, void *ws = nullptr,
     const double c256 = tile_cost(t256, 1, 256, 256, g.K, 1.0, p256);
     const double c192 = tile_cost(t192, 1, 192, 256, g.K, 0.9, p192);
     const double c128 = tile_cost(t128, 2, 128, 128, g.K, 0.8, p128);
+    const bool fits = (size_t)(g.M + 256) * g.K * 2 < ((size_t)1 << 31) &&
+                      (size_t)g.N * g.K * 2 < ((size_t)1 << 31);
+    // Small grids (the 256 x 256 tiles fill at most one round, K <= 4096, no
+    // SwiGLU): 128 x 128 tiles, two blocks per CU, on 16x16x32 MFMA tiles
+    // with buffer loads and no K split. The vision tower's M = 1728 GEMMs
+    // (K = 1152): 11.5-20 us against 22-27 us on the previous choice (128 x
+    // 128 tiles on 32x32x16 MFMA with a 4-chunk K split); a 1152-token
+    // block's o_proj: equal at block level (507 us per block either way).
+    // Longer K (the 12288-deep down projection) and the SwiGLU epilogue stay
+    // on the 256-row tiles (120 vs 139-150 us; 192-212 vs 208-223 us).
+    const int slots1 = gemm_slots() > 0 ? gemm_slots() : 256;
+    if (g_family != 1 && g_family != 3 && fits && EPI != EPI_SWIGLU && t256 <= slots1 && g.K <= 4096) {
+        if (launch) launch_ms<128, 128, 64, 2, 2, 2, EPI, 8, 2, 5, 16>(g);
+        return "bf16_128x128x64_w2x2_occ2_m16";
+    }
     if (c128 < c256 && c128 < c192) {
+        if (g_family != 1 && fits) {
+            if (launch) launch_ms<128, 128, 64, 2, 2, 2, EPI, 8, 2, 5, 16>(g, ws, ws_bytes);
+            return p128 > 1 ? "bf16_128x128x64_w2x2_occ2_m16_split" : "bf16_128x128x64_w2x2_occ2_m16";
+        }
         if (launch) launch_ms<128, 128, 64, 2, 2, 2, EPI, 1, 2>(g, ws, ws_bytes);
         return p128 > 1 ? "bf16_128x128x64_w2x2_occ2_split" : "bf16_128x128x64_w2x2_occ2";
     }
@@ -1617,8 +1639,6 @@ static const char *pick_and_launch(GemmArgs &g, bool launch, void *ws = nullptr,
     // rings (schedule 3; the same K order, bit-identical). Family 1: the
     // previous production kernels on v_mfma_f32_32x32x16_bf16 (kept for
     // same-process comparisons).
-    const bool fits = (size_t)(g.M + 256) * g.K * 2 < ((size_t)1 << 31) &&
-                      (size_t)g.N * g.K * 2 < ((size_t)1 << 31);
     const bool use192 = c192 < c256;
     const bool split256 = p256 > 1;
     if (g_family == 2 && fits) {

@@ -252,3 +252,50 @@ def test_mfma_probe_checksums(pkg, lib, dev, shape):
                                  pkg.ptr(out)) == 0
         with pytest.raises(RuntimeError, match="mfma_probe: bad args"):
             pkg.check_prim("mfma_probe")   # reports through the error buffer, then clears it
+
+
+@pytest.mark.parametrize("M,N,K,epi,use_ws", [(1728, 1152, 1152, 0, False), (1728, 3456, 1152, 2, True),
+                                              (1728, 1152, 4352, 0, True), (700, 1536, 1024, 3, True),
+                                              (1152, 4096, 4096, 2, True)])
+def test_small_grid_128_tiles(pkg, lib, dev, M, N, K, epi, use_ws):
+    """Small grids run on 128x128 tiles (two blocks per CU, 16x16x32 MFMA):
+    without a K split when the 256-row grid fits one round and K <= 4096, and
+    through the cost model (with its tail split when a workspace is given)
+    otherwise: the vision tower's M = 1728 shapes, a ragged SwiGLU and the
+    one-block o_proj shape, against torch fp32 (one bf16 rounding of the
+    product, then the epilogue's own)."""
+    print(f"small grid M={M} N={N} K={K} epi={epi} ws={use_ws} "
+          f"cfg={lib.hd_gemm_config_name(M, N, K, epi).decode()}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(M + N + K)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    wu = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    r = torch.randn(M, N, generator=g, device=dev).to(torch.bfloat16)
+    ws = torch.empty(lib.hd_gemm_ws_bytes(), dtype=torch.uint8, device=dev)
+    wp, wn = (pkg.ptr(ws), ws.numel()) if use_ws else (None, 0)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    prod = (x.float() @ w.float().t()).to(torch.bfloat16).float()
+    if epi == 0:
+        lib.hd_linear_ws(pkg.ptr(x), pkg.ptr(w), None, pkg.ptr(y), M, N, K, wp, wn)
+        want = prod
+    elif epi == 2:
+        lib.hd_linear_residual_ws(pkg.ptr(x), pkg.ptr(w), pkg.ptr(r), pkg.ptr(y), M, N, K, wp, wn)
+        want = (prod + r.float()).to(torch.bfloat16).float()
+    else:
+        lib.hd_linear_swiglu_ws(pkg.ptr(x), pkg.ptr(w), pkg.ptr(wu), pkg.ptr(y), M, N, K, wp, wn)
+        up = (x.float() @ wu.float().t()).to(torch.bfloat16).float()
+        sg = (prod * torch.sigmoid(prod)).to(torch.bfloat16).float()
+        want = (sg * up).to(torch.bfloat16).float()
+    pkg.check_prim("small grid gemm")
+    torch.cuda.synchronize()
+    got = y.float().cpu()
+    want = want.cpu()
+    assert rel_l2(got, want) < 5e-3
+    assert cosine(got, want) > 0.99999
+    if epi == 2:
+        # a step of the rounded product survives the residual add even
+        # where the sum cancels: the bound scales with |product| + |sum|
+        step = (prod.abs().cpu() + want.abs()) * 2.0 ** -7 * 2 + 1e-6
+        assert bool(((got - want).abs() <= step).all())
+    else:
+        assert close_bf16(got.numpy(), want.numpy(), ulps=2 if epi == 0 else 4, atol_rel=1e-3)
