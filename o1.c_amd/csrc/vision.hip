@@ -196,42 +196,92 @@ __global__ void v_cos_sin_kernel(const uint16_t *__restrict__ rot, float *__rest
 }
 
 // qkv [R*n, 3, heads, D] (R images of n rows) -> q, k (rotary applied in
-// fp32, one rounding, rope.cu:157-180) and v, head-major [R, heads, n, DP]
-// with columns [D, DP) zero: the flash kernel's head_dim-128 operands. One
-// thread per output element of q, k and v.
-__global__ void v_qkv_rope_pad_kernel(const uint16_t *__restrict__ qkv, const float *__restrict__ cosd,
-                                      const float *__restrict__ sind, uint16_t *__restrict__ q,
-                                      uint16_t *__restrict__ k, uint16_t *__restrict__ v, int R,
-                                      int n, int heads, int D, int DP) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)R * heads * n * DP) return;
-    const int d = (int)(i % DP);
-    const int s = (int)((i / DP) % n), h = (int)((i / ((size_t)DP * n)) % heads);
-    const int img = (int)(i / ((size_t)DP * n * heads));
-    if (d >= D) {
-        q[i] = 0;
-        k[i] = 0;
-        v[i] = 0;
-        return;
+// fp32, one rounding, rope.cu:157-180), head-major [R, heads, n, DP] with
+// columns [D, DP) zero (the flash kernel's head_dim-128 operands), and v
+// written straight into the flash kernel's V^T operand [R*heads, DP, S_pad]
+// (64-key tiles whose storage column p holds key p with bits 2 and 3
+// exchanged; rows d >= D and keys >= n zero). One block per (64-row tile,
+// image, head) stages the tile's q, k and v slices in LDS; 16-byte loads and
+// stores. v itself (head-major like q) is written only when v_out is not
+// null (the block-0 snapshots). D = 72, DP = 128 (D % 8 == 0, and the
+// 144-byte head slices keep 16-byte alignment).
+__global__ __launch_bounds__(256) void v_qkv_rope_vt_kernel(
+    const uint16_t *__restrict__ qkv, const float *__restrict__ cosd, const float *__restrict__ sind,
+    uint16_t *__restrict__ q, uint16_t *__restrict__ k, uint16_t *__restrict__ vt,
+    uint16_t *__restrict__ v_out, int n, int s_pad) {
+    constexpr int D = kD, DP = kDP, CH = D / 8, LD = D + 8;
+    static_assert(D % 8 == 0 && D <= DP && DP % 8 == 0, "16-byte head slices");
+    __shared__ __attribute__((aligned(16))) uint16_t t[3][64][LD];
+    const int s0 = blockIdx.x * 64, h = blockIdx.y % kNH, img = blockIdx.y / kNH;
+    const int bh = blockIdx.y;
+    for (int i = threadIdx.x; i < 3 * 64 * CH; i += 256) {
+        const int part = i / (64 * CH), r = (i / CH) % 64, c = (i % CH) * 8;
+        u32x4_t val = {0, 0, 0, 0};
+        if (s0 + r < n)
+            val = *(const u32x4_t *)(qkv + ((size_t)img * n + s0 + r) * 3 * kNH * D +
+                                     (size_t)(part * kNH + h) * D + c);
+        *(u32x4_t *)&t[part][r][c] = val;
     }
-    const int half = D / 2, dp = d < half ? d + half : d - half;
-    const size_t row = ((size_t)img * n + s) * 3 * heads * D;
-    const float c = cosd[(size_t)s * D + d], sn = sind[(size_t)s * D + d];
-    const uint16_t *qs = qkv + row + (size_t)h * D, *ks = qs + (size_t)heads * D;
-    const float q0 = bf2f(qs[d]), qh = bf2f(qs[dp]), k0 = bf2f(ks[d]), kh = bf2f(ks[dp]);
-    q[i] = f2bf(d < half ? q0 * c - qh * sn : q0 * c + qh * sn);
-    k[i] = f2bf(d < half ? k0 * c - kh * sn : k0 * c + kh * sn);
-    v[i] = ks[(size_t)heads * D + d];
+    __syncthreads();
+    const int half = D / 2;
+    // q, k: rows [s0, s0 + 64) x 16 chunks of 8 columns (chunks >= CH zero)
+    for (int i = threadIdx.x; i < 64 * (DP / 8); i += 256) {
+        const int r = i / (DP / 8), c = (i % (DP / 8)) * 8, srow = s0 + r;
+        if (srow >= n) continue;
+        const size_t o = ((size_t)bh * n + srow) * DP + c;
+        u32x4_t oq = {0, 0, 0, 0}, ok = {0, 0, 0, 0};
+        if (c < D) {
+            uint16_t rq[8], rk[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int d = c + e, dp = d < half ? d + half : d - half;
+                const float cc = cosd[(size_t)srow * D + d], sn = sind[(size_t)srow * D + d];
+                const float q0 = bf2f(t[0][r][d]), qh = bf2f(t[0][r][dp]);
+                const float k0 = bf2f(t[1][r][d]), kh = bf2f(t[1][r][dp]);
+                rq[e] = f2bf(d < half ? q0 * cc - qh * sn : q0 * cc + qh * sn);
+                rk[e] = f2bf(d < half ? k0 * cc - kh * sn : k0 * cc + kh * sn);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                oq[e] = (uint32_t)rq[2 * e] | ((uint32_t)rq[2 * e + 1] << 16);
+                ok[e] = (uint32_t)rk[2 * e] | ((uint32_t)rk[2 * e + 1] << 16);
+            }
+        }
+        *(u32x4_t *)(q + o) = oq;
+        *(u32x4_t *)(k + o) = ok;
+        if (v_out) {
+            u32x4_t ov = {0, 0, 0, 0};
+            if (c < D) ov = *(const u32x4_t *)&t[2][r][c];
+            *(u32x4_t *)(v_out + o) = ov;
+        }
+    }
+    // V^T: rows d < DP, 8 chunks of 8 storage columns of this 64-key tile
+    for (int i = threadIdx.x; i < DP * 8; i += 256) {
+        const int d = i / 8, p0 = (i % 8) * 8;
+        u32x4_t ov = {0, 0, 0, 0};
+        if (d < D) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int pa = p0 + 2 * e, pb = pa + 1;
+                const int ka = (pa & ~12) | ((pa & 4) << 1) | ((pa & 8) >> 1);
+                const int kb = (pb & ~12) | ((pb & 4) << 1) | ((pb & 8) >> 1);
+                ov[e] = (uint32_t)t[2][ka][d] | ((uint32_t)t[2][kb][d] << 16);
+            }
+        }
+        *(u32x4_t *)(vt + ((size_t)bh * DP + d) * s_pad + s0 + p0) = ov;
+    }
 }
 
-// flash output [n, heads*DP] (seq-major) -> [n, heads*D]
+// flash output [n, heads*DP] (seq-major) -> [n, heads*D]; one thread per
+// 8 consecutive columns (D % 8 == 0)
 __global__ void v_unpad_heads_kernel(const uint16_t *__restrict__ in, uint16_t *__restrict__ out,
                                      int n, int heads, int D, int DP) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)n * heads * D) return;
-    const int d = (int)(i % D), h = (int)((i / D) % heads);
-    const size_t s = i / ((size_t)D * heads);
-    out[i] = in[(s * heads + h) * DP + d];
+    const int cpr = D / 8;
+    if (i >= (size_t)n * heads * cpr) return;
+    const int c = (int)(i % cpr) * 8, h = (int)((i / cpr) % heads);
+    const size_t s = i / ((size_t)cpr * heads);
+    *(u32x4_t *)(out + (s * heads + h) * D + c) = *(const u32x4_t *)(in + (s * heads + h) * DP + c);
 }
 
 // rows x cols -> rows x ld, columns [cols, ld) zero (cols, ld % 8 == 0)
@@ -746,21 +796,20 @@ static hd_status forward_impl(const hd_vision_binding *bw, hd_vision_workspace *
         }
         hd_linear_ws(ln, b->qkv_w, b->qkv_b, qkv, N, kQKV, kH, gws, gwsb);
         if (s0) snap(s0[HD_B0_QKV], qkv, (size_t)N * kQKV * 2);
-        v_qkv_rope_pad_kernel<<<hd_cdiv((size_t)R * kNH * n * kDP, 256), 256, 0, st>>>(
-            qkv, cs, sn, q, k, v, R, n, kNH, kD, kDP);
+        v_qkv_rope_vt_kernel<<<dim3((unsigned)((n + 63) / 64), (unsigned)(R * kNH)), 256, 0, st>>>(
+            qkv, cs, sn, q, k, vt, s0 ? v : nullptr, n, (int)((n + 63) / 64 * 64));
         if (s0) {
             snap(s0[HD_B0_Q], q, (size_t)R * kNH * n * kDP * 2);
             snap(s0[HD_B0_K], k, (size_t)R * kNH * n * kDP * 2);
             snap(s0[HD_B0_V], v, (size_t)R * kNH * n * kDP * 2);
         }
-        hd_flash_make_vt(v, vt, R * kNH, n);
         // full attention per image over the zero-padded heads; output
         // [R*n, 16*128] (seq-major) into qkv
         if (hd_flash_attention(q, k, vt, nullptr, qkv, R, kNH, kNH, n, kDP, 0, scale, 1)) {
             hd_set_error("vision: attention failed: %s", hd_cuda_last_error());
             return HD_ERR_RUNTIME;
         }
-        v_unpad_heads_kernel<<<hd_cdiv((size_t)N * kH, 256), 256, 0, st>>>(qkv, ln, N, kNH, kD, kDP);
+        v_unpad_heads_kernel<<<hd_cdiv((size_t)N * kH / 8, 256), 256, 0, st>>>(qkv, ln, N, kNH, kD, kDP);
         if (s0) snap(s0[HD_B0_ATTN_MERGED], ln, nH);
         hd_linear_ws(ln, b->proj_w, b->proj_b, tmp, N, kH, kH, gws, gwsb);
         if (s0) snap(s0[HD_B0_PROJ], tmp, nH);
