@@ -1368,15 +1368,18 @@ __global__ __launch_bounds__(64) void gemm_tail_qkv_epi_kernel(GemmArgs g, int n
     qkv_epilogue<RS, LDW>(g, stg, tm * BM + sl * RS, (tn * BN) / 128 + hc, lane);
 }
 
-// Resident blocks of one round (one GEMM block per CU).
-// EPI_QKV tail tiles in one pass: one wave per (tile, 64-row slice, head)
+// Rows per wave of the fused QKV tail (32: 22.6 vs 23.6 us with 64 for a
+// 1152-token block's all-split grid, equal at 8704 rows).
+constexpr int QKV_TAIL_RS = 32;
+
+// EPI_QKV tail tiles in one pass: one wave per (tile, RS-row slice, head)
 // sums the K chunks' fp32 partials of its rows (in chunk order, as
 // gemm_tail_merge_kernel does), stages the bf16 projection in LDS exactly as
 // gemm_ms_kernel stages it and runs the same qkv_epilogue; no bf16 staging
 // round trip through memory and one launch instead of two.
-template <int BM, int BN>
+template <int BM, int BN, int RS>
 __global__ __launch_bounds__(64) void gemm_tail_qkv_fused_kernel(GemmArgs g, int n_tail) {
-    constexpr int RS = 64, LDW = 128 + 8, GROUP_M = 8, NSL = BM / RS, NH = BN / 128;
+    constexpr int LDW = 128 + 8, GROUP_M = 8, NSL = BM / RS, NH = BN / 128;
     __shared__ __attribute__((aligned(16))) uint16_t stg[RS * LDW];
     const int lane = threadIdx.x;
     const int b = blockIdx.x;
@@ -1415,6 +1418,7 @@ __global__ __launch_bounds__(64) void gemm_tail_qkv_fused_kernel(GemmArgs g, int
     qkv_epilogue<RS, LDW>(g, stg, tm * BM + sl * RS, (tn * BN) / 128 + hc, lane);
 }
 
+// Resident blocks of one round (one GEMM block per CU).
 static int gemm_slots() {
     static int dev_cached = -1, cus = 0;
     int dev = 0;
@@ -1463,9 +1467,9 @@ static void launch_ms(GemmArgs &g, void *ws = nullptr, int64_t ws_bytes = 0) {
     gemm_ms_kernel<BM, BN, BK, NS, WGM, WGN, EPI, SGB, OCC, LDR, MF>
         <<<(unsigned)(g.n_whole + n_tail * P), Cfg::NT, 0, hd_stream()>>>(g);
     if (n_tail) {
-        if constexpr (EPI == EPI_QKV && BM % 64 == 0) {
-            gemm_tail_qkv_fused_kernel<BM, BN>
-                <<<(unsigned)(n_tail * (BM / 64) * (BN / 128)), 64, 0, hd_stream()>>>(g, (int)n_tail);
+        if constexpr (EPI == EPI_QKV && BM % QKV_TAIL_RS == 0) {
+            gemm_tail_qkv_fused_kernel<BM, BN, QKV_TAIL_RS>
+                <<<(unsigned)(n_tail * (BM / QKV_TAIL_RS) * (BN / 128)), 64, 0, hd_stream()>>>(g, (int)n_tail);
         } else {
             gemm_tail_merge_kernel<BM, BN, WGN, EPI>
                 <<<hd_cdiv((size_t)n_tail * BM * (Cfg::BN_OUT / 4), 256), 256, 0, hd_stream()>>>(
