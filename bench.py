@@ -9,8 +9,11 @@ A "step" = one hd_forward_batched call over both CFG sequences.
 
 Prints ONE JSON line (driver contract) with roofline and cpu_baseline. The
 default run also times, on the same weights, configuration 2 (2048x2048,
-16640 tokens, batch 1) as a `c2` object and configuration 0 (one block,
-S = 1152) as a `c0` object.
+16640 tokens, batch 1) as a `c2` object, configuration 0 (one block,
+S = 1152) as a `c0` object, configuration 3 (the edit step: 1024^2 target
++ 3 references, 16896 tokens, vision conditioning) as a `c3` object and,
+last because it rewrites the weights, configuration 4 (GPU LoRA merge into
+all 252 projection weights + one 28-step CFG image) as a `c4` object.
 """
 import argparse
 import ctypes
@@ -67,6 +70,13 @@ def main():
                     help="with the default configuration 1, skip the configuration 0 (one block, "
                          "S = 1152) timing that the same run adds as its `c0` object")
     ap.add_argument("--c0-steps", type=int, default=200)
+    ap.add_argument("--no-c3", action="store_true",
+                    help="with the default configuration 1, skip the configuration 3 (edit step, "
+                         "1024^2 target + 3 references, vision conditioning) object")
+    ap.add_argument("--c3-steps", type=int, default=5)
+    ap.add_argument("--no-c4", action="store_true",
+                    help="with the default configuration 1, skip the configuration 4 (LoRA merge + "
+                         "28-step CFG image) object; it merges into the model's weights, so it runs last")
     ap.add_argument("--kernel-iters", type=int, default=20)
     ap.add_argument("--flash-only", action="store_true",
                     help="run only the flash attention kernel at the configuration's shape "
@@ -99,6 +109,9 @@ def main():
     from importlib import import_module
     synth = import_module("o1c_amd.synthetic")
 
+    # random-init weights leave the reference's [-2, 2] final-latent range:
+    # the 28-step image keeps only the NaN/Inf part of the fail-closed check
+    lib.hd_denoise_set_output_check(1)
     cfg = CFGS[args.config]
     B, T, gh, gw, R = cfg["batch"], cfg["text"], cfg["gh"], cfg["gw"], cfg["refs"]
     I = gh * gw * (1 + R)
@@ -200,6 +213,26 @@ def main():
                      "block_tflops": round(r0["flops"] / (r0["ms"] * 1e-3) / 1e12, 1),
                      "block_mfma_frac": round(r0["flops"] / (r0["ms"] * 1e-3) / PEAK_BF16, 4),
                      "wall_s": round(r0["wall"], 3), "gemm": r0["gemm"]}
+    if args.config == "c1" and not args.no_c3:
+        # configuration 3: the edit step (512 text + 64x64 target + 3
+        # references of 64x64, S = 16896) with vision conditioning
+        print("[bench] configuration 3 (edit step, 3 references) on the same model", file=sys.stderr, flush=True)
+        r3 = time_config(pkg, lib, synth, model, tensors, "c3", args.c3_steps, 2, args.layers,
+                         args.kernel_iters, dev, args)
+        c3 = CFGS["c3"]
+        res["c3"] = {"workload": c3["name"], "seq_len": c3["text"] + c3["gh"] * c3["gw"] * (1 + c3["refs"]),
+                     "batch": 1, "steps": args.c3_steps, "ms_per_step": round(r3["ms"], 3),
+                     "steps_per_s": round(1000.0 / r3["ms"], 4), "step_tflops": r3["step_tflops"],
+                     "step_mfma_frac": r3["step_mfma_frac"], "wall_s": r3["wall_s"],
+                     "gemm": r3["gemm"], "attention": r3["attention"], **r3["extra"]}
+    if args.config == "c1" and not args.no_c4:
+        # configuration 4 last: the LoRA merge rewrites the model's weights
+        print("[bench] configuration 4 (LoRA merge + 28-step image) on the same model", file=sys.stderr,
+              flush=True)
+        r4 = time_config(pkg, lib, synth, model, tensors, "c4", 3, 1, args.layers, args.kernel_iters, dev, args)
+        c4 = CFGS["c4"]
+        res["c4"] = {"workload": c4["name"], "seq_len": c4["text"] + c4["gh"] * c4["gw"], "batch": 2,
+                     "ms_per_step": round(r4["ms"], 3), **r4["extra"]}
     print(json.dumps(res))
 
 

@@ -157,6 +157,16 @@ hd_status hd_denoise_euler_cfg(const hd_forward_binding *bw, hd_forward_workspac
                                int hidden, int ff_hidden, int head_dim, int tms_token_id,
                                void *scratch, int64_t scratch_bytes, void *stream);
 
+/* Final-latent check of every denoise loop (generate.c:1474-1496): after the
+ * last step the loop returns HD_ERR_MISSING (generate's failure status,
+ * generate.c:1546) with hd_last_error() set when the latent holds a NaN/Inf
+ * ("final latent contains NaN/Inf") or, in mode 2, a value outside [-2, 2]
+ * ("final latent range [lo, hi] out of bounds"); z keeps the values the last
+ * step wrote. mode 2 = the reference's check (default), 1 = NaN/Inf only
+ * (random-weight runs leave the range), 0 = off. Process-wide; returns the
+ * previous mode, or -1 for a mode outside 0..2. */
+int hd_denoise_set_output_check(int mode);
+
 /* hd_denoise: the reference's three samplers on the device.
  *   HD_SAMPLER_EULER  flow_match: z = bf16(z + (s_{i+1} - s_i) mo)
  *   HD_SAMPLER_FLASH  dev/flash SDE: per-step noise (hd_step_noise from

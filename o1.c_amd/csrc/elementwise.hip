@@ -1164,3 +1164,71 @@ extern "C" void hd_patchify_bf16(const float *img, void *tok, int C, int Hp, int
     launch_patch<0, uint16_t>(img, (uint16_t *)tok, C, Hp, Wp, p);
     hd_check_launch("patchify_bf16");
 }
+
+// ---------------------------------------------------------------------------
+// Final-latent check (generate.c:1474-1496 fails closed on the raw output):
+// per block, the count of NaN/Inf values and the min / max of the finite ones
+// over a bf16 latent. Block b writes part[3b .. 3b+2]; the host folds the
+// `blocks` triples. Grid-stride over 16-byte chunks (8 values per lane) with
+// a scalar tail, so any n and alignment of 2 bytes is accepted.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void latent_stats_kernel(const uint16_t *__restrict__ z, int64_t n,
+                                                           float *__restrict__ part) {
+    float bad = 0.f, mn = INFINITY, mx = -INFINITY;
+    auto one = [&](uint32_t bits16) {
+        const float v = __uint_as_float(bits16 << 16);
+        if ((bits16 & 0x7F80u) == 0x7F80u) {
+            bad += 1.f;
+        } else {
+            mn = fminf(mn, v);
+            mx = fmaxf(mx, v);
+        }
+    };
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t nthr = (int64_t)gridDim.x * blockDim.x;
+    int64_t done = 0;
+    if (((uintptr_t)z & 15) == 0) {
+        const int64_t nch = n / 8;
+        for (int64_t c = tid; c < nch; c += nthr) {
+            const u32x4_t v = *(const u32x4_t *)(z + c * 8);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                one(v[e] & 0xFFFFu);
+                one(v[e] >> 16);
+            }
+        }
+        done = nch * 8;
+    }
+    for (int64_t i = done + tid; i < n; i += nthr) one(z[i]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        bad += __shfl_xor(bad, o, 64);
+        mn = fminf(mn, __shfl_xor(mn, o, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    }
+    __shared__ float red[4][3];
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        red[w][0] = bad;
+        red[w][1] = mn;
+        red[w][2] = mx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = red[0][0], lo = red[0][1], hi = red[0][2];
+        for (int k = 1; k < (int)(blockDim.x >> 6); k++) {
+            b += red[k][0];
+            lo = fminf(lo, red[k][1]);
+            hi = fmaxf(hi, red[k][2]);
+        }
+        part[3 * blockIdx.x] = b;
+        part[3 * blockIdx.x + 1] = lo;
+        part[3 * blockIdx.x + 2] = hi;
+    }
+}
+// Internal (host.cpp): `blocks` <= HD_LATENT_STAT_BLOCKS partial triples.
+extern "C" void hd_latent_stats(const void *z, int64_t n, float *part, int blocks) {
+    if (!z || !part || n <= 0 || blocks <= 0) BAD("latent_stats");
+    latent_stats_kernel<<<blocks, 256, 0, hd_stream()>>>((const uint16_t *)z, n, part);
+    hd_check_launch("latent_stats");
+}

@@ -20,6 +20,7 @@
 #include <stdlib.h>
 #include <string.h>
 #include <math.h>
+#include <atomic>
 #include <type_traits>
 
 #include "hd_common.hpp"
@@ -1947,7 +1948,9 @@ extern "C" void hd_linear_ws(const void *x, const void *w, const void *bias, voi
 static constexpr int64_t kNoAllocScratchBytes = (int64_t)256 * 256 * 256 * 4 + 128 * 256 * 256 * 2;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 static constexpr int kMaxDevices = 64;
-static void *g_scratch_dev[kMaxDevices];   // the array's device address, per device
+// the array's device address, per device; atomic slots, since two host
+// threads may look the address up at once (both store the same value)
+static std::atomic<void *> g_scratch_dev[kMaxDevices];
 
 extern "C" int64_t hd_linear_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
 
@@ -1959,7 +1962,8 @@ extern "C" void hd_linear_noalloc(const void *x, const void *w, const void *bias
                  kMaxDevices);
         return;
     }
-    if (!g_scratch_dev[dev]) {
+    void *sp = g_scratch_dev[dev].load(std::memory_order_acquire);
+    if (!sp) {
         // once per device, with that device current: the host-side name of
         // the array is not its device address
         void *p = nullptr;
@@ -1969,7 +1973,8 @@ extern "C" void hd_linear_noalloc(const void *x, const void *w, const void *bias
                      hipGetErrorString(e));
             return;
         }
-        g_scratch_dev[dev] = p;
+        g_scratch_dev[dev].store(p, std::memory_order_release);
+        sp = p;
     }
     const int64_t need = hd_gemm_ws_bytes();
     if (need > kNoAllocScratchBytes) {
@@ -1979,7 +1984,7 @@ extern "C" void hd_linear_noalloc(const void *x, const void *w, const void *bias
                  (long long)need, (long long)kNoAllocScratchBytes);
         return;
     }
-    hd_linear_ws(x, w, bias, y, M, N, K, g_scratch_dev[dev], kNoAllocScratchBytes);
+    hd_linear_ws(x, w, bias, y, M, N, K, sp, kNoAllocScratchBytes);
 }
 
 // hd_linear writing rows of stride ldc (>= N, ldc % 8 == 0): the vision

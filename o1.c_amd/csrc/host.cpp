@@ -6,6 +6,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
+
 #include "../../include/hd_hip.h"
 #include "../../include/hd_host.h"
 
@@ -494,12 +496,64 @@ extern "C" void hd_decode_to_rgb(const float *z, int gh, int gw, int p, int C, u
 static inline int64_t al256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 static const float kTEps = 1e-6f;   // sigma floor of the velocity division (generate.c:64)
 
+// ---------------------------------------------------------------------------
+// Final-latent check. The reference's generate fails closed on the raw output
+// latent (generate.c:1474-1496): any NaN/Inf, or a value outside [-2, 2],
+// sets the error and returns its failure status (generate.c:1546). The
+// loops below run the same check after their last step: mode 2 (default) is
+// the reference's check, 1 keeps only the NaN/Inf test (random-weight runs
+// leave the [-2, 2] range), 0 switches it off.
+// ---------------------------------------------------------------------------
+extern "C" void hd_latent_stats(const void *z, int64_t n, float *part, int blocks);
+static constexpr int kLatentStatBlocks = 256;
+static std::atomic<int> g_output_check{2};
+
+extern "C" int hd_denoise_set_output_check(int mode) {
+    if (mode < 0 || mode > 2) return -1;
+    return g_output_check.exchange(mode);
+}
+
+static int64_t latent_check_bytes() { return al256((int64_t)kLatentStatBlocks * 3 * 4); }
+
+// z: [n] bf16 on the device; part: device scratch of latent_check_bytes()
+static hd_status check_final_latent(const void *z, int64_t n, float *part, hipStream_t st) {
+    const int mode = g_output_check.load();
+    if (mode == 0 || n <= 0) return HD_OK;
+    const int64_t want = (n + 2047) / 2048;
+    const int blocks = (int)(want < kLatentStatBlocks ? want : kLatentStatBlocks);
+    hd_cuda_clear_error();
+    hd_latent_stats(z, n, part, blocks);
+    float h[kLatentStatBlocks * 3];
+    if (hd_cuda_last_error()[0] ||
+        hipMemcpyAsync(h, part, (size_t)blocks * 3 * 4, hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess) {
+        hd_set_error("denoise: final latent check failed to run");
+        return HD_ERR_RUNTIME;
+    }
+    float bad = 0.f, mn = INFINITY, mx = -INFINITY;
+    for (int b = 0; b < blocks; b++) {
+        bad += h[3 * b];
+        mn = fminf(mn, h[3 * b + 1]);
+        mx = fmaxf(mx, h[3 * b + 2]);
+    }
+    if (bad > 0.f) {
+        hd_set_error("denoise: final latent contains NaN/Inf");
+        return HD_ERR_MISSING;   // generate.c's failure status (generate.c:1546)
+    }
+    if (mode == 2 && (mn < -2.0f || mx > 2.0f)) {
+        hd_set_error("denoise: final latent range [%.4f, %.4f] out of bounds", mn, mx);
+        return HD_ERR_MISSING;
+    }
+    return HD_OK;
+}
+
 extern "C" int64_t hd_denoise_scratch_bytes(int seq, int img, int steps) {
     const int64_t n = (int64_t)img * 3072;
     return al256(2 * n * 2)                       // vin [2, I, 3072] bf16
            + al256((int64_t)2 * seq * 3072 * 2)   // x_pred [2, S, 3072] bf16
            + al256(3 * n * 4)                     // mo_c, mo_u, mo fp32
-           + al256((int64_t)(steps + 1) * 2 * 4); // t pairs
+           + al256((int64_t)(steps + 1) * 2 * 4)  // t pairs
+           + latent_check_bytes();                // final-latent check partials
 }
 
 extern "C" hd_status hd_denoise_euler_cfg(const hd_forward_binding *bw, hd_forward_workspace *ws,
@@ -524,7 +578,8 @@ extern "C" hd_status hd_denoise_euler_cfg(const hd_forward_binding *bw, hd_forwa
     uint16_t *vin = (uint16_t *)p; p += al256(2 * n * 2);
     uint16_t *xp = (uint16_t *)p; p += al256((int64_t)2 * S * 3072 * 2);
     float *mo_c = (float *)p, *mo_u = mo_c + n, *mo = mo_u + n; p += al256(3 * n * 4);
-    float *tdev = (float *)p;
+    float *tdev = (float *)p; p += al256((int64_t)(steps + 1) * 2 * 4);
+    float *chk = (float *)p;
     hd_status status = HD_OK;
     if (steps > HD_SCHED_MAX_STEPS) {
         hd_set_error("denoise: too many steps");
@@ -555,6 +610,7 @@ extern "C" hd_status hd_denoise_euler_cfg(const hd_forward_binding *bw, hd_forwa
             status = HD_ERR_RUNTIME;
         }
     }
+    if (status == HD_OK) status = check_final_latent(z, n, chk, st);
     hd_hip_set_stream(prev);
     return status;
 }
@@ -570,7 +626,8 @@ extern "C" int64_t hd_denoise_run_scratch_bytes(int B, int S, int I, int steps) 
            + al256(7 * n * 4)                        // sampler state (UniPC: z, 3 conv slots,
                                                      // last, corrected, predicted; flash: noise
                                                      // + the step's 3n scratch)
-           + al256((int64_t)(steps + 1) * B * 4);    // timesteps
+           + al256((int64_t)(steps + 1) * B * 4)     // timesteps
+           + latent_check_bytes();                   // final-latent check partials
 }
 
 namespace {
@@ -629,7 +686,8 @@ static hd_status denoise_loop(const hd_forward_binding *bw, hd_forward_workspace
     uint16_t *xp_u = xp + (size_t)S_rows * 3072;
     float *mo_c = (float *)p, *mo_u = mo_c + n, *mo = mo_u + n; p += al256(3 * n * 4);
     float *st = (float *)p; p += al256(7 * n * 4);
-    float *tdev = (float *)p;
+    float *tdev = (float *)p; p += al256((int64_t)(steps + 1) * B * 4);
+    float *chk = (float *)p;
 
     PinnedNoise pn;
     hd_torch_rng rng;
@@ -762,6 +820,7 @@ static hd_status denoise_loop(const hd_forward_binding *bw, hd_forward_workspace
             status = HD_ERR_RUNTIME;
         }
     }
+    if (status == HD_OK) status = check_final_latent(z, n, chk, hs);
     hd_hip_set_stream(prev_stream);
     return status;
 }

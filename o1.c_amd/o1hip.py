@@ -334,6 +334,7 @@ SIGNATURES = {
     "hd_scheduler_unipc_step": (c_int, [ctypes.POINTER(hd_scheduler), ctypes.POINTER(hd_scheduler_unipc),
                                         P, P, P, c_int, P]),
     "hd_step_noise": (None, [ctypes.POINTER(hd_torch_rng), P, c_int64, c_float]),
+    "hd_denoise_set_output_check": (c_int, [c_int]),
     "hd_denoise_run_scratch_bytes": (c_int64, [c_int, c_int, c_int, c_int]),
     "hd_denoise": (c_int, [ctypes.POINTER(hd_forward_binding), ctypes.POINTER(hd_forward_workspace), c_int,
                            ctypes.POINTER(hd_scheduler), c_int, c_int, P, c_int, P, c_int, P, c_int,

@@ -45,5 +45,9 @@ def _restore_block_config(request):
     lb = request.getfixturevalue("lib")
     saved = pk.hd_block_config()
     lb.hd_block_get_config(ctypes.byref(saved))
+    # random-weight loops leave the reference's [-2, 2] final-latent range:
+    # keep only the NaN/Inf part of the fail-closed check unless a test sets it
+    prev_check = lb.hd_denoise_set_output_check(1)
     yield
     lb.hd_block_set_config(ctypes.byref(saved))
+    lb.hd_denoise_set_output_check(prev_check)

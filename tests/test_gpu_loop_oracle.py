@@ -34,7 +34,9 @@ STEPS = 3
 
 
 def oracle_loop(fw, cfg, seqs, z0, sig, guidance, sampler, seed=0, clip=0.0, sn=(1.0, 1.0), unipc=None):
-    """seqs: [(ids, pos, T)] - one (conditional) or two (+ unconditional).
+    """seqs: [(ids, pos, T)] or [(ids, pos, T, cfg)] - one (conditional) or
+    two (+ unconditional); a fourth item overrides `cfg` for that sequence
+    (its own causal prefix).
     unipc: (lib, pkg, sched) for sampler 2 - the per-step plan comes from
     hd_scheduler_unipc_plan (host code pinned bit-exact against the
     reference's scheduler.c by the CPU tests)."""
@@ -48,8 +50,9 @@ def oracle_loop(fw, cfg, seqs, z0, sig, guidance, sampler, seed=0, clip=0.0, sn=
         sg = max(float(s_i), 1e-6)
         t = float(np.float32(1.0) - s_i)
         mos = []
-        for ids, pos, T in seqs:
-            xp = orc.forward(fw, cfg, ids, z, t, pos, TMS)[T:]
+        for sq in seqs:
+            ids, pos, T = sq[:3]
+            xp = orc.forward(fw, sq[3] if len(sq) > 3 else cfg, ids, z, t, pos, TMS)[T:]
             mos.append(orc.sched_vcond(z, xp, sg))
         mo = orc.sched_cfg_guided(mos[0], mos[1], guidance) if len(mos) == 2 else mos[0]
         if sampler == 0:
@@ -161,7 +164,7 @@ def test_denoise_cfg_equal_length_vs_oracle_loop(pkg, lib, dev, sampler):
     lib.hd_forward_binding_free(ctypes.byref(fb))
 
 
-@pytest.mark.parametrize("sampler", [0, 1])
+@pytest.mark.parametrize("sampler", [0, 1, 2])
 def test_denoise_cfg_own_uncond_sequence_vs_oracle_loop(pkg, lib, dev, sampler):
     """hd_denoise_cfg: the unconditional branch is a shorter sequence of its
     own (the reference's " " caption), with its own positions and
@@ -172,7 +175,10 @@ def test_denoise_cfg_own_uncond_sequence_vs_oracle_loop(pkg, lib, dev, sampler):
     ids, idu = ids_for(T, 3), ids_for(Tu, 4)
     pos, posu = grid_pos(T, GH, GW), grid_pos(Tu, GH, GW)
     sch = pkg.hd_scheduler()
-    lib.hd_scheduler_derive_flash(ctypes.byref(sch), STEPS, 3.0, 8.0)
+    if sampler == 2:   # FlowUniPC: the reference's default schedule (generate.c:1335-1345)
+        lib.hd_scheduler_derive_default(ctypes.byref(sch), STEPS, 3.0, 8.0)
+    else:
+        lib.hd_scheduler_derive_flash(ctypes.byref(sch), STEPS, 3.0, 8.0)
     sig = [sch.sigmas[i] for i in range(sch.num_steps)]
     z0 = bf16(torch.randn(I, 3072, generator=torch.Generator().manual_seed(6))).numpy()
     g, seed, clip, sn = 5.0, 91, 2.0, (1.0, 0.5)
@@ -191,12 +197,13 @@ def test_denoise_cfg_own_uncond_sequence_vs_oracle_loop(pkg, lib, dev, sampler):
     torch.cuda.synchronize()
     z = zd.float().cpu().numpy()
     sq = [(ids, pos, T), (idu, posu, Tu)]
-    zo = oracle_loop(ofw, cfg[0], sq, z0, sig, g, sampler, seed, clip, sn)
-    zo32 = oracle_loop(ofw, cfg[1], sq, z0, sig, g, sampler, seed, clip, sn)
+    up = (lib, pkg, sch)
+    zo = oracle_loop(ofw, cfg[0], sq, z0, sig, g, sampler, seed, clip, sn, unipc=up)
+    zo32 = oracle_loop(ofw, cfg[1], sq, z0, sig, g, sampler, seed, clip, sn, unipc=up)
     compare(z, z0, zo, zo32, f"hd_denoise_cfg sampler {sampler}")
     # padding the unconditional prompt to the conditional length is not the same
     zp = oracle_loop(ofw, cfg[0], [(ids, pos, T), (np.concatenate([idu, ids_for(T - Tu, 4)]), pos, T)],
-                     z0, sig, g, sampler, seed, clip, sn)
+                     z0, sig, g, sampler, seed, clip, sn, unipc=up)
     assert rel_l2(zp - z0, zo - z0) > 2e-2
     # argument checks return before any device call
     assert lib.hd_denoise_cfg(ctypes.byref(fb), ctypes.byref(ws), ctypes.byref(ws), sampler, ctypes.byref(sch),
@@ -238,4 +245,152 @@ def test_denoise_unguided_vs_oracle_loop(pkg, lib, dev):
     r, c = rel_l2(d, do), cosine(d, do)
     print(f"unguided: update rel_l2={r:.3e} cos={c:.7f}", flush=True)
     assert r <= 1e-2 and c >= 0.9999, (r, c)
+    lib.hd_forward_binding_free(ctypes.byref(fb))
+
+
+def test_denoise_cfg_causal_prefixes_vs_oracle_loop(pkg, lib, dev):
+    """hd_denoise_cfg with the reference's text-to-image masks on both
+    branches: each sequence's text rows attend causally (rows < T - 1 see
+    keys <= row; generate.c:1119-1120 builds maskd[0] and maskd[1] with
+    ar_len = text_len - 1 each), through each workspace's own split plan."""
+    keep, fb, ofw, cfg = setup(pkg, lib, dev)
+    T, Tu = 20, 6
+    S, Su = T + I, Tu + I
+    ids, idu = ids_for(T, 13), ids_for(Tu, 14)
+    pos, posu = grid_pos(T, GH, GW), grid_pos(Tu, GH, GW)
+    sch = pkg.hd_scheduler()
+    lib.hd_scheduler_derive_flash(ctypes.byref(sch), STEPS, 3.0, 8.0)
+    sig = [sch.sigmas[i] for i in range(sch.num_steps)]
+    z0 = bf16(torch.randn(I, 3072, generator=torch.Generator().manual_seed(16))).numpy()
+    g = 5.0
+    ws, wb = workspace(pkg, lib, dev, 1, S)
+    wsu, wbu = workspace(pkg, lib, dev, 1, Su)
+    sb = lib.hd_denoise_cfg_scratch_bytes(S, Su, I, STEPS)
+    scratch = torch.empty(sb, dtype=torch.uint8, device=dev)
+    zd = torch.from_numpy(z0).to(dev, torch.bfloat16)
+    dv = lambda a: torch.from_numpy(a).to(dev)
+    idsd, idud, posd, posud = dv(ids), dv(idu), dv(pos), dv(posu)
+    st = lib.hd_denoise_cfg(ctypes.byref(fb), ctypes.byref(ws), ctypes.byref(wsu), 0, ctypes.byref(sch),
+                            STEPS, pkg.ptr(idsd), T, pkg.ptr(posd), T - 1, S, pkg.ptr(idud), Tu, pkg.ptr(posud),
+                            Tu - 1, Su, pkg.ptr(zd), I, g, 0, 1.0, 1.0, 0.0, H, KV, HID, FF, D, TMS,
+                            pkg.ptr(scratch), sb, None)
+    pkg.check_status(st, "hd_denoise_cfg (causal prefixes)")
+    torch.cuda.synchronize()
+    z = zd.float().cpu().numpy()
+    mk = lambda ar, faithful: orc.block_cfg(H, KV, HID, FF, D, theta=1e4, faithful=faithful, ar_len=ar)
+    sq = [(ids, pos, T, mk(T - 1, 1)), (idu, posu, Tu, mk(Tu - 1, 1))]
+    sq32 = [(ids, pos, T, mk(T - 1, 0)), (idu, posu, Tu, mk(Tu - 1, 0))]
+    zo = oracle_loop(ofw, cfg[0], sq, z0, sig, g, 0)
+    zo32 = oracle_loop(ofw, cfg[1], sq32, z0, sig, g, 0)
+    compare(z, z0, zo, zo32, "hd_denoise_cfg causal prefixes")
+    # the prefixes matter: the same loop with full attention is a different result
+    zf = oracle_loop(ofw, cfg[0], [(ids, pos, T), (idu, posu, Tu)], z0, sig, g, 0)
+    assert rel_l2(zf - z0, zo - z0) > 1e-3
+    lib.hd_forward_binding_free(ctypes.byref(fb))
+
+
+@pytest.mark.parametrize("loop", ["hd_denoise", "hd_denoise_cfg"])
+def test_first_guided_velocity_vs_oracle(pkg, lib, dev, loop):
+    """The guided velocity of one step, where the device loop and the oracle
+    see the same latent, at the north-star bound (rel-L2 <= 1e-2, cosine >=
+    0.9999). One Euler step from sigma 1 to 0 gives z1 = bf16(z0 - mo), so
+    z0 - z1 is the guided velocity (5 mo_c - 4 mo_u) up to the bf16 rounding
+    of z1, which the oracle applies too."""
+    keep, fb, ofw, cfg = setup(pkg, lib, dev)
+    sch = pkg.hd_scheduler()
+    pkg.check_status(lib.hd_scheduler_init(ctypes.byref(sch), (ctypes.c_float * 2)(1.0, 0.0), 2, 0.0),
+                     "scheduler")
+    z0 = bf16(torch.randn(I, 3072, generator=torch.Generator().manual_seed(21))).numpy()
+    zd = torch.from_numpy(z0).to(dev, torch.bfloat16)
+    dv = lambda a: torch.from_numpy(a).to(dev)
+    g = 5.0
+    if loop == "hd_denoise":
+        T = Tu = 16
+        ids, idu = ids_for(T, 22), ids_for(T, 23)
+        pos = posu = grid_pos(T, GH, GW)
+        S = T + I
+        ws, wbuf = workspace(pkg, lib, dev, 2, S)
+        sb = lib.hd_denoise_run_scratch_bytes(2, S, I, 1)
+        scratch = torch.empty(sb, dtype=torch.uint8, device=dev)
+        idsd, posd = dv(np.stack([ids, idu])), dv(pos)
+        st = lib.hd_denoise(ctypes.byref(fb), ctypes.byref(ws), 0, ctypes.byref(sch), 1, 2, pkg.ptr(idsd), T,
+                            pkg.ptr(posd), 0, pkg.ptr(zd), I, g, 0, 1.0, 1.0, 0.0, S, H, KV, HID, FF, D, TMS,
+                            pkg.ptr(scratch), sb, None)
+    else:
+        T, Tu = 20, 6
+        ids, idu = ids_for(T, 24), ids_for(Tu, 25)
+        pos, posu = grid_pos(T, GH, GW), grid_pos(Tu, GH, GW)
+        S, Su = T + I, Tu + I
+        ws, wb = workspace(pkg, lib, dev, 1, S)
+        wsu, wbu = workspace(pkg, lib, dev, 1, Su)
+        sb = lib.hd_denoise_cfg_scratch_bytes(S, Su, I, 1)
+        scratch = torch.empty(sb, dtype=torch.uint8, device=dev)
+        idsd, idud, posd, posud = dv(ids), dv(idu), dv(pos), dv(posu)
+        st = lib.hd_denoise_cfg(ctypes.byref(fb), ctypes.byref(ws), ctypes.byref(wsu), 0, ctypes.byref(sch), 1,
+                                pkg.ptr(idsd), T, pkg.ptr(posd), 0, S, pkg.ptr(idud), Tu, pkg.ptr(posud), 0, Su,
+                                pkg.ptr(zd), I, g, 0, 1.0, 1.0, 0.0, H, KV, HID, FF, D, TMS, pkg.ptr(scratch),
+                                sb, None)
+    pkg.check_status(st, loop)
+    torch.cuda.synchronize()
+    v = z0 - zd.float().cpu().numpy()
+    xc = orc.forward(ofw, cfg[0], ids, z0, 0.0, pos, TMS)[T:]
+    xu = orc.forward(ofw, cfg[0], idu, z0, 0.0, posu, TMS)[Tu:]
+    mo = orc.sched_cfg_guided(orc.sched_vcond(z0, xc, 1.0), orc.sched_vcond(z0, xu, 1.0), g)
+    vo = z0 - orc.sched_flow_match_step(z0, mo, 1.0, 0.0)
+    r, c = rel_l2(v, vo), cosine(v, vo)
+    print(f"{loop}: first guided velocity rel_l2={r:.3e} cos={c:.7f}", flush=True)
+    assert r <= 1e-2 and c >= 0.9999, (r, c)
+    lib.hd_forward_binding_free(ctypes.byref(fb))
+
+
+def test_final_latent_fails_closed(pkg, lib, dev):
+    """generate.c:1474-1496: a NaN/Inf in the final latent, or (the
+    reference's default check) a value outside [-2, 2], fails the loop with
+    HD_ERR_MISSING (generate.c:1546) and the reference's message. One Euler
+    step with sigma 1 -> 1 leaves z = bf16(z + 0 * mo) = z, so the final
+    latent is the input the test chose."""
+    keep, fb, ofw, cfg = setup(pkg, lib, dev)
+    sch = pkg.hd_scheduler()
+    pkg.check_status(lib.hd_scheduler_init(ctypes.byref(sch), (ctypes.c_float * 2)(1.0, 1.0), 2, 0.0),
+                     "scheduler")
+    T = 16
+    S = T + I
+    ids, pos = ids_for(T, 31), grid_pos(T, GH, GW)
+    ws, wbuf = workspace(pkg, lib, dev, 1, S)
+    sb = lib.hd_denoise_run_scratch_bytes(1, S, I, 1)
+    scratch = torch.empty(sb, dtype=torch.uint8, device=dev)
+    idsd, posd = torch.from_numpy(ids).to(dev), torch.from_numpy(pos).to(dev)
+    base = torch.rand(I, 3072, generator=torch.Generator().manual_seed(32)) * 3.0 - 1.5   # [-1.5, 1.5)
+
+    def run(z, mode):
+        assert lib.hd_denoise_set_output_check(mode) in (0, 1, 2)
+        zd = z.to(dev, torch.bfloat16)
+        st = lib.hd_denoise(ctypes.byref(fb), ctypes.byref(ws), 0, ctypes.byref(sch), 1, 1, pkg.ptr(idsd), T,
+                            pkg.ptr(posd), 0, pkg.ptr(zd), I, 1.0, 0, 1.0, 1.0, 0.0, S, H, KV, HID, FF, D, TMS,
+                            pkg.ptr(scratch), sb, None)
+        torch.cuda.synchronize()
+        return st, lib.hd_last_error().decode(), zd
+
+    st, msg, zd = run(base, 2)
+    assert st == pkg.HD_OK, msg
+    assert torch.equal(zd.cpu(), base.to(torch.bfloat16))      # sigma 1 -> 1 keeps z
+    hi = base.clone()
+    hi[10, 7] = 2.5
+    st, msg, _ = run(hi, 2)
+    assert st == pkg.HD_ERR_MISSING and "out of bounds" in msg and "2.5000" in msg, (st, msg)
+    lo = base.clone()
+    lo[5, 3000] = -2.25
+    st, msg, _ = run(lo, 2)
+    assert st == pkg.HD_ERR_MISSING and "[-2.2500," in msg, (st, msg)
+    assert run(hi, 1)[0] == pkg.HD_OK           # mode 1: NaN/Inf only
+    nan = base.clone()
+    nan[I - 1, 3071] = float("nan")
+    st, msg, _ = run(nan, 1)
+    assert st == pkg.HD_ERR_MISSING and "NaN/Inf" in msg, (st, msg)
+    inf = base.clone()
+    inf[0, 0] = float("inf")
+    st, msg, _ = run(inf, 2)
+    assert st == pkg.HD_ERR_MISSING and "NaN/Inf" in msg, (st, msg)
+    assert run(nan, 0)[0] == pkg.HD_OK          # mode 0: off
+    assert lib.hd_denoise_set_output_check(3) == -1
     lib.hd_forward_binding_free(ctypes.byref(fb))
