@@ -49,7 +49,7 @@ void hd_linear(const void *x_dev, const void *w_dev, const void *bias_dev,
 /* gemm.h:61 - 1 = production (MFMA, default), 0 = reference kernel. */
 void hd_gemm_set_backend(int use_production);
 /* gemm.h:67 - accepted for source compatibility; there is one production
- * kernel family, so the value is recorded and otherwise ignored. */
+ * kernel family, so the value is ignored. */
 void hd_gemm_set_prod_backend(int backend);
 
 /* Extension: hd_linear (transpose_w = 1) writing rows of stride ldc >= N
@@ -105,13 +105,6 @@ void hd_linear_concat3(const void *x_dev, const void *w0, int N0,
                        const void *w1, int N1, const void *w2, int N2,
                        void *y_dev, int M, int K);
 
-/* Diagnostics/tuning: launches tuning-table configuration `cfg` (0..35)
- * with epilogue 0 (plain, N outputs) or 3 (SwiGLU: w0 = gate, w1 = up, N =
- * F outputs). Returns 0 when launched, non-zero for an unknown config or
- * unsupported shape. */
-int hd_gemm_tune_run(int cfg, int epi, const void *x, const void *w0, const void *w1, void *y,
-                     int M, int N, int K);
-
 /* Extension (diagnostic, no counterpart in the reference): matrix-core
  * ceiling probe. `blocks` blocks of 8 waves each run 8 independent
  * v_mfma_f32_32x32x16_bf16 chains (shape 32) or 16 v_mfma_f32_16x16x32_bf16
@@ -142,19 +135,6 @@ int hd_linear_qkv_rope_ws(const void *x, const void *wq, const void *wk, const v
                           const void *qn_w, const void *kn_w, const float *cs, void *q, void *k,
                           void *vt, int batch, int seq, int heads, int kv_heads, int hidden,
                           float eps, void *ws, int64_t ws_bytes);
-
-/* Diagnostics/tuning: kernel family for the production GEMMs. 0 (default):
- * 8-wave fragment-ring tiles on v_mfma_f32_16x16x32_bf16 with buffer loads
- * for every K (the fused QKV epilogue included), the A operand's LDS ring
- * three stages deep and B's two; 2: the same tiles with both rings two
- * stages deep (identical values to 0); 1: the previous kernels on
- * v_mfma_f32_32x32x16_bf16 (the same split rings; the fused QKV epilogue on
- * 4-wave tiles), which sum each output's K products in 16-wide instead of
- * 32-wide groups (values within fp32 reassociation of family 0); 3: family 0
- * without the small-grid rule (grids of 256 x 256 tiles that fit one round,
- * K <= 4096, no SwiGLU: 128 x 128 tiles, two blocks per CU, no K split), for
- * comparisons. Returns the previous value. */
-int hd_gemm_set_family(int family);
 
 #ifdef __cplusplus
 }

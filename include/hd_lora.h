@@ -79,17 +79,6 @@ const char *hd_lora_last_error(void);
  * rank above 256, HD_ERR_RUNTIME on a launch failure. */
 hd_status hd_lora_merge_gpu(hd_lora_entry *entries, size_t count, void *stream);
 
-/* Extension: merge kernel selection for same-process comparisons.
- * 0 (default) = the streaming kernel where it applies (rank <= 64, rank % 4
- * == 0, in_dim % 8 == 0, W under 2 GiB): the rank product on the bf16 matrix
- * cores with each fp32 operand split in three bf16 parts (fp32-grade
- * products; the delta agrees with an fp32 SGEMM up to summation order),
- * else family 1; 1 = the fp32 matrix-core kernel (v_mfma_f32_32x32x2_f32),
- * rank loop unrolled; 2 = the same, rolled (identical results to 1);
- * 3 = the split-operand product in one block per tile (the same part
- * products, one accumulator: equal to 0 up to fp32 summation order).
- * Returns the previous setting. */
-int hd_lora_set_family(int family);
 
 #ifdef __cplusplus
 }

@@ -81,16 +81,6 @@ int hd_flash_attention(const void *q, const void *k, const void *vt,
 int hd_flash_attention_ws(const void *q, const void *k, const void *vt, const void *mask,
                           void *out, int batch, int q_heads, int kv_heads, int seq, int head_dim,
                           int ar_len, float scale, int out_seq_major, void *ws, int64_t ws_bytes);
-/* Extension (tuning): flash kernel family. 1 = blocks of 4 waves (128
- * queries, two blocks per CU); 2 = blocks of 8 waves (256 queries, one block
- * per CU, one copy of each K / V^T tile for all of them) in lockstep; 3 = the
- * 8-wave blocks as a ping-pong (the two waves of each SIMD alternate MFMA and
- * softmax phases, one phase apart); 4 = the ping-pong on
- * v_mfma_f32_16x16x32_bf16 tiles; 0 (default) = automatic: family 4 with a
- * tail-split workspace, full attention and S >= 1024, else 1. Families 1-3
- * compute identical values; family 4 sums the same products in 32-wide
- * groups (values within fp32 reassociation). Returns the previous value. */
-int hd_flash_set_family(int family);
 /* Workspace bytes for the tail split on the current device (one round of
  * resident flash blocks x 128 rows x (128 + 2) floats). */
 int64_t hd_flash_ws_bytes(void);

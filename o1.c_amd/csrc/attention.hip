@@ -16,9 +16,10 @@
 //    fetch is one 16-byte LDS read;
 //  * K and V^T tiles go global -> LDS with buffer_load_dwordx4 ... lds into two
 //    buffers (64 keys per tile), XOR-swizzled by row.
-// The 8-wave blocks run flash_pp_kernel, the same arithmetic split into
-// alternating MFMA and softmax phases with the two waves of each SIMD one
-// phase apart (four LDS tile buffers, loads two tiles ahead).
+// The 8-wave blocks run flash_pp16_kernel: the same online softmax on
+// v_mfma_f32_16x16x32_bf16 tiles, split into alternating MFMA and softmax
+// phases with the two waves of each SIMD one phase apart (four LDS tile
+// buffers, loads two tiles ahead).
 //
 // vt layout: [B, Hkv, 128, S_pad] bf16, S_pad = round_up(S, 64), key s
 // stored at column perm16(s) = s with bits 2 and 3 exchanged, padding zero.
@@ -343,7 +344,7 @@ __global__ __launch_bounds__(NWV * 64, 8 / NWV) void flash_fwd_kernel(FaArgs a) 
 }
 
 // Ping-pong form of the 8-wave kernel. Each wave alternates an MFMA phase
-// (O += P(t-1) V(t-1) and S(t) = K(t) Q^T: 32 MFMAs) with a softmax phase
+// (O += P(t-1) V(t-1) and S(t) = K(t) Q^T) with a softmax phase
 // (max, lazy rescale, exp2, P(t): VALU only). Waves w and w + 4 share a SIMD;
 // waves 4..7 run one phase behind waves 0..3, so on every SIMD one wave's
 // softmax issues while the other wave's MFMAs run. A block barrier closes
@@ -358,304 +359,9 @@ __device__ __forceinline__ void fa_barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool MASKED>
-__global__ __launch_bounds__(512, 1) void flash_pp_kernel(FaArgs a) {
-    constexpr int BQ = 256, LPW = 2, NB = 4;
-    __shared__ __attribute__((aligned(1024))) uint16_t smem[NB * (FA_BK * FA_D + FA_D * FA_BK)];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int grp = wave >> 2;
-    const int l32 = lane & 31, h = lane >> 5;
-
-    const int nqt = (a.q_row_end - a.q_row_begin + BQ - 1) / BQ;
-    const int group = a.Hq / a.Hkv;
-    int lin = blockIdx.x, chunk = -1, item = 0;
-    if (lin >= a.n_whole) {
-        item = lin - a.n_whole;
-        chunk = item % a.split;
-        lin = a.n_whole + item / a.split;
-    } else {
-        lin = fa_xcd_remap(lin, a.n_whole);
-    }
-    const int g = lin % group; lin /= group;
-    const int qt = lin % nqt; lin /= nqt;
-    const int hk = lin % a.Hkv;
-    const int b = lin / a.Hkv;
-    const int hq = hk * group + g;
-
-    const int qb = a.q_row_begin + qt * BQ;
-    const int q0 = qb + wave * 32;
-    const int my_q = q0 + l32;
-    const bool causal_block = qb < a.ar_len;
-    int kv_end = a.S;
-    if (causal_block) {
-        int last_row = min(qb + BQ, a.q_row_end) - 1;
-        if (last_row < a.ar_len) kv_end = last_row + 1;
-    }
-    int t_begin = 0, t_end = (kv_end + FA_BK - 1) / FA_BK;
-    if (chunk >= 0) {
-        const int nt = t_end;
-        t_begin = chunk * nt / a.split;
-        t_end = (chunk + 1) * nt / a.split;
-    }
-
-    const uint16_t *qrow = a.q + (((size_t)b * a.Hq + hq) * a.S + min(my_q, a.S - 1)) * FA_D;
-    bf16x8_t qf[8];
-#pragma unroll
-    for (int ks = 0; ks < 8; ks++) qf[ks] = *(const bf16x8_t *)(qrow + ks * 16 + h * 8);
-
-    const uint16_t *kbase = a.k + ((size_t)b * a.Hkv + hk) * (size_t)a.S * FA_D;
-    const uint16_t *vbase = a.vt + ((size_t)b * a.Hkv + hk) * (size_t)FA_D * a.S_pad;
-    // buffer i: K at smem + i * 8192, V^T at smem + (NB + i) * 8192; same
-    // swizzles as the kernel above
-    uint16_t *Ks0 = smem, *Vs0 = smem + NB * FA_BK * FA_D;
-    const int kbytes = a.S * FA_D * 2, vbytes = FA_D * a.S_pad * 2;
-    uint32_t k_vo[LPW], v_vo[LPW];
-#pragma unroll
-    for (int i = 0; i < LPW; i++) {
-        const int krow = (wave * LPW + i) * 4 + (lane >> 4);
-        k_vo[i] = (uint32_t)(krow * FA_D + (((lane & 15) ^ (krow & 15)) * 8)) * 2;
-        const int vrow = (wave * LPW + i) * 8 + (lane >> 3);
-        v_vo[i] = (uint32_t)(vrow * a.S_pad + (((lane & 7) ^ ((vrow >> 1) & 7)) * 8)) * 2;
-    }
-    auto issue = [&](int t) {
-        const int buf = t & (NB - 1);
-        uint16_t *Ks = Ks0 + buf * FA_BK * FA_D, *Vs = Vs0 + buf * FA_D * FA_BK;
-#pragma unroll
-        for (int i = 0; i < LPW; i++)
-            fa_buf_load16(kbase, kbytes, k_vo[i], (uint32_t)t * FA_BK * FA_D * 2,
-                          (HD_LDS void *)(Ks + (wave * LPW + i) * 512));
-#pragma unroll
-        for (int i = 0; i < LPW; i++)
-            fa_buf_load16(vbase, vbytes, v_vo[i], (uint32_t)t * FA_BK * 2,
-                          (HD_LDS void *)(Vs + (wave * LPW + i) * 512));
-    };
-
-    f32x16_t o[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) o[i][r] = 0.f;
-    float m_run = -1e30f, l_run = 0.f;
-    f32x16_t s[2];
-    bf16x8_t pf[4];
-
-    // S(t) = K(t) Q^T
-    auto qk = [&](int t) {
-        const uint16_t *Ks = Ks0 + (t & (NB - 1)) * FA_BK * FA_D;
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) s[j][r] = 0.f;
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++)
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int row = j * 32 + l32;
-                const int c = ((ks * 2 + h) ^ (row & 15)) * 8;
-                bf16x8_t kf = *(const bf16x8_t *)(Ks + row * FA_D + c);
-                s[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[j], 0, 0, 0);
-            }
-    };
-    // O += V^T(t) P(t)^T
-    auto pv = [&](int t) {
-        const uint16_t *Vs = Vs0 + (t & (NB - 1)) * FA_D * FA_BK;
-#pragma unroll
-        for (int st = 0; st < 4; st++)
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++) {
-                const int row = dt * 32 + l32;
-                const int c = ((st * 2 + h) ^ ((row >> 1) & 7)) * 8;
-                bf16x8_t vf = *(const bf16x8_t *)(Vs + row * FA_BK + c);
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[st], o[dt], 0, 0, 0);
-            }
-    };
-    // both products of one MFMA phase, interleaved (independent chains)
-    auto pv_qk = [&](int t) {
-        const uint16_t *Vs = Vs0 + ((t - 1) & (NB - 1)) * FA_D * FA_BK;
-        const uint16_t *Ks = Ks0 + (t & (NB - 1)) * FA_BK * FA_D;
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) s[j][r] = 0.f;
-#pragma unroll
-        for (int st = 0; st < 4; st++)
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++) {
-                const int vrow = dt * 32 + l32;
-                const int vc = ((st * 2 + h) ^ ((vrow >> 1) & 7)) * 8;
-                bf16x8_t vf = *(const bf16x8_t *)(Vs + vrow * FA_BK + vc);
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[st], o[dt], 0, 0, 0);
-                const int ks = st * 2 + (dt >> 1), j = dt & 1;
-                const int krow = j * 32 + l32;
-                const int kc = ((ks * 2 + h) ^ (krow & 15)) * 8;
-                bf16x8_t kf = *(const bf16x8_t *)(Ks + krow * FA_D + kc);
-                s[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[j], 0, 0, 0);
-            }
-        // fragment reads run FA_PF reads ahead of the MFMAs: one wave per SIMD
-        // issues MFMAs in this phase, so nothing else hides the LDS latency
-        __builtin_amdgcn_sched_group_barrier(0x100, FA_PF, 0);
-#pragma unroll
-        for (int i = 0; i < 32 - FA_PF; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, FA_PF, 0);
-    };
-    // softmax of S(t) into P(t), with the lazy O rescale
-    auto softmax = [&](int t) {
-        const int kv0 = t * FA_BK;
-        const bool need_mask = MASKED && (a.mask != nullptr || kv0 + FA_BK > a.S ||
-                                          (q0 < a.ar_len && kv0 + FA_BK - 1 > q0));
-        float mt = -INFINITY;
-        if (need_mask) {
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    float v = s[j][r];
-                    const int kv = kv0 + j * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                    bool dead = kv >= a.S || (my_q < a.ar_len && kv > my_q);
-                    if (a.mask && !dead && my_q < a.S)
-                        v += bf2f(a.mask[(size_t)my_q * a.S + kv]) * a.inv_scale;
-                    if (dead) v = -INFINITY;
-                    s[j][r] = v;
-                    mt = fmaxf(mt, v);
-                }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) mt = fmaxf(mt, s[j][r]);
-        }
-        mt = xor32_max(mt);
-        if (__builtin_amdgcn_ballot_w64((mt - m_run) * a.scale_log2 > FA_TAU)) {
-            const float m_new = fmaxf(m_run, mt);
-            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * a.scale_log2);
-            m_run = m_new;
-            l_run *= alpha;
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) o[i][r] *= alpha;
-        }
-        const float mc = -m_run * a.scale_log2;
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int hh = 0; hh < 2; hh++) {
-                bf16x8_t pv8;
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    float p = __builtin_amdgcn_exp2f(fmaf(s[j][hh * 8 + e], a.scale_log2, mc));
-                    l_run += p;
-                    pv8[e] = (__bf16)p;
-                }
-                pf[j * 2 + hh] = pv8;
-            }
-    };
-    // the softmax results are consumed only after the next barrier; this
-    // empty asm uses them, so their computation stays in the softmax phase
-    auto pin_softmax = [&]() {
-        asm volatile("" ::"v"(pf[0]), "v"(pf[1]), "v"(pf[2]), "v"(pf[3]), "v"(l_run));
-    };
-    // loads of this wave still in flight after the ones for the next tile:
-    // the tile issued in this phase (LPW K + LPW V^T instructions) or none
-    auto wait_next = [&](bool issued) {
-        if (issued) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-        else fa_wait_vm0();
-    };
-
-    // The epilogue's pointers are loaded and consumed here: a scalar load
-    // still in flight inside the loop would make every LDS wait there a
-    // full drain (scalar loads complete out of order)
-    {
-        float *part = a.part;
-        uint16_t *outp = a.out;
-        asm volatile("" ::"s"(part), "s"(outp));
-    }
-    // Barrier sequence (every wave executes 2T + 3 barriers, T = tiles):
-    //   group 0: P  M0 |  V0 M1 | V1 ... M(T-1) | V(T-1) M(T) | epilogue X
-    //   group 1: P  X  M0 | V0 M1 | ...          | V(T-1) M(T) | epilogue
-    // (P: after the first loads, X: the extra barrier that offsets group 1).
-    issue(t_begin);
-    if (t_begin + 1 < t_end) {
-        issue(t_begin + 1);
-        wait_next(true);
-    } else {
-        fa_wait_vm0();
-    }
-    fa_barrier();
-    if (grp) fa_barrier();
-    {   // M(0): S(t_begin) only
-        const bool ld = t_begin + 2 < t_end;
-        if (ld) issue(t_begin + 2);
-        qk(t_begin);
-        wait_next(ld);
-        fa_barrier();
-    }
-    for (int t = t_begin + 1; t < t_end; t++) {
-        softmax(t - 1);
-        pin_softmax();
-        fa_barrier();
-        const bool ld = t + 2 < t_end;
-        if (ld) issue(t + 2);
-        pv_qk(t);
-        wait_next(ld);
-        fa_barrier();
-    }
-    softmax(t_end - 1);
-    pin_softmax();
-    fa_barrier();
-    pv(t_end - 1);
-    fa_barrier();
-
-    // ---- normalise and store (same layout as the kernel above) -------------
-    const float l_tot = xor32_sum(l_run);
-    if (chunk >= 0) {
-        float *po = a.part + ((size_t)item * BQ + wave * 32 + l32) * FA_D;
-#pragma unroll
-        for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-            for (int gq = 0; gq < 4; gq++) {
-                const int d = dt * 32 + gq * 8 + h * 4;
-                *(f32x4_t *)(po + d) = {o[dt][gq * 4], o[dt][gq * 4 + 1], o[dt][gq * 4 + 2],
-                                        o[dt][gq * 4 + 3]};
-            }
-        if (h == 0) {
-            float2 *pml = (float2 *)(a.part + (size_t)(gridDim.x - a.n_whole) * BQ * FA_D);
-            pml[(size_t)item * BQ + wave * 32 + l32] = make_float2(m_run, l_tot);
-        }
-    } else if (my_q < a.q_row_end) {
-        const float inv = 1.0f / l_tot;
-        uint16_t *dst;
-        if (a.out_seq_major)
-            dst = a.out + (((size_t)b * a.out_rows + my_q) * a.Hq + hq) * FA_D;
-        else
-            dst = a.out + (((size_t)b * a.Hq + hq) * a.out_rows + my_q) * FA_D;
-#pragma unroll
-        for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-            for (int gp = 0; gp < 2; gp++) {
-                const int g0 = 2 * gp, g1 = g0 + 1;
-                const u32x2_t p0 = {pack_bf2(o[dt][g0 * 4] * inv, o[dt][g0 * 4 + 1] * inv),
-                                    pack_bf2(o[dt][g0 * 4 + 2] * inv, o[dt][g0 * 4 + 3] * inv)};
-                const u32x2_t p1 = {pack_bf2(o[dt][g1 * 4] * inv, o[dt][g1 * 4 + 1] * inv),
-                                    pack_bf2(o[dt][g1 * 4 + 2] * inv, o[dt][g1 * 4 + 3] * inv)};
-                const uint32_t z0 = h ? p0[0] : p1[0], z1 = h ? p0[1] : p1[1];
-                const auto s0 = __builtin_amdgcn_permlane32_swap(z0, z0, false, false);
-                const auto s1 = __builtin_amdgcn_permlane32_swap(z1, z1, false, false);
-                const uint32_t r0 = h ? s0[0] : s0[1], r1 = h ? s1[0] : s1[1];
-                const u32x4_t v = h ? (u32x4_t){r0, r1, p1[0], p1[1]} : (u32x4_t){p0[0], p0[1], r0, r1};
-                *(u32x4_t *)(dst + dt * 32 + (h ? g1 : g0) * 8) = v;
-            }
-    }
-    if (!grp) fa_barrier();
-}
-
-// 16x16x32 form of the ping-pong kernel (the automatic 8-wave choice). The
-// same phases, barriers, LDS buffers and loads as flash_pp_kernel; each
-// wave's 32 queries are two 16-query blocks, and every product runs on
+// The ping-pong kernel (the automatic 8-wave choice) on 16x16x32 tiles: the
+// phases, barriers, LDS buffers and loads above; each wave's 32 queries are
+// two 16-query blocks, and every product runs on
 // v_mfma_f32_16x16x32_bf16 (under the power limit the matrix cores sustain
 // more FLOP/s with it on random operands than with 32x32x16):
 //  * S^T = K Q^T: 4 MFMAs of 16 keys per tile and query block, each summing
@@ -917,7 +623,7 @@ __global__ __launch_bounds__(512, 1) void flash_pp16_kernel(FaArgs a) {
         uint16_t *outp = a.out;
         asm volatile("" ::"s"(part), "s"(outp));
     }
-    // barrier sequence as in flash_pp_kernel (2T + 3 barriers per wave)
+    // the barrier sequence of the phases above (2T + 3 barriers per wave)
     issue(t_begin);
     if (t_begin + 1 < t_end) {
         issue(t_begin + 1);
@@ -1051,7 +757,7 @@ static int fa_slots(int nwv = 4) {
         int per4 = 0, per8 = 0, cus = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per4, flash_fwd_kernel<false, 4>, 256, 0) !=
                 hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per8, flash_pp_kernel<false>, 512, 0) !=
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per8, flash_pp16_kernel<false>, 512, 0) !=
                 hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             return 0;
@@ -1060,19 +766,6 @@ static int fa_slots(int nwv = 4) {
         dev_cached = dev;
     }
     return nwv == 8 ? slots8 : slots4;
-}
-
-// hd_flash_set_family: 0 = automatic (below), 1 = 4-wave blocks, 2 = 8-wave
-// blocks in lockstep (flash_fwd_kernel), 3 = 8-wave ping-pong blocks on
-// 32x32x16 MFMA tiles (flash_pp_kernel), 4 = 8-wave ping-pong blocks on
-// 16x16x32 tiles (flash_pp16_kernel, the automatic choice for 8 waves).
-// Families 1-3 run the same per-row arithmetic (bit-identical); family 4
-// sums the same products in 32-wide instead of 16-wide groups.
-static int g_fa_family = 0;
-extern "C" int hd_flash_set_family(int family) {
-    const int prev = g_fa_family;
-    g_fa_family = family >= 1 && family <= 4 ? family : 0;
-    return prev;
 }
 
 // Workspace for the tail split: at most one round of partial blocks.
@@ -1110,8 +803,7 @@ static int fa_launch(const void *q, const void *k, const void *vt, const void *m
     // full attention in the unmasked kernel with the tail split. One masked
     // launch over all rows costs 7-12 % more: its block holding row ar_len
     // runs every key with most of its waves masked, and it has no split.
-    if (ar_len > 0 && !mask && ws && q_row_begin == 0 && (seq % FA_BK) == 0 && ar_len < q_row_end &&
-        g_fa_family == 0) {
+    if (ar_len > 0 && !mask && ws && q_row_begin == 0 && (seq % FA_BK) == 0 && ar_len < q_row_end) {
         const int rc = fa_launch(q, k, vt, nullptr, out, batch, hq, hkv, seq, ar_len, ar_len, scale,
                                  out_seq_major, st, nullptr, 0, out_rows, 0);
         if (rc) return rc;
@@ -1140,11 +832,7 @@ static int fa_launch(const void *q, const void *k, const void *vt, const void *m
     // amortise the larger block: +3 % at S = 16640 / 16896, equal at 4352;
     // 4-wave blocks otherwise (without the split their finer grain wins)
     const bool split_ok = ws && !mask && ar_len == 0;
-    const int nwv = g_fa_family == 1 ? 4 : g_fa_family >= 2 ? 8 : (split_ok && seq >= 1024 ? 8 : 4);
-    // the ping-pong form: +2.5-4.7 % at S = 4352-16640 over the lockstep
-    // blocks; on 16x16x32 MFMA tiles unless family 3 asks for 32x32x16
-    const bool pp = nwv == 8 && g_fa_family != 2;
-    const bool pp16 = pp && g_fa_family != 3;
+    const int nwv = split_ok && seq >= 1024 ? 8 : 4;
     const int BQ = nwv * 32;
     const int nqt = (q_row_end - q_row_begin + BQ - 1) / BQ;
     const int units = batch * hq * nqt;
@@ -1169,15 +857,11 @@ static int fa_launch(const void *q, const void *k, const void *vt, const void *m
         }
     }
     dim3 grid((unsigned)(a.n_whole + n_tail * a.split));
-    if (pp16) {
+    if (nwv == 8) {
+        // the ping-pong form: +2.5-4.7 % at S = 4352-16640 over 8-wave
+        // blocks in lockstep
         if (masked) flash_pp16_kernel<true><<<grid, 512, 0, st>>>(a);
         else flash_pp16_kernel<false><<<grid, 512, 0, st>>>(a);
-    } else if (pp) {
-        if (masked) flash_pp_kernel<true><<<grid, 512, 0, st>>>(a);
-        else flash_pp_kernel<false><<<grid, 512, 0, st>>>(a);
-    } else if (nwv == 8) {
-        if (masked) flash_fwd_kernel<true, 8><<<grid, 512, 0, st>>>(a);
-        else flash_fwd_kernel<false, 8><<<grid, 512, 0, st>>>(a);
     } else {
         if (masked) flash_fwd_kernel<true, 4><<<grid, 256, 0, st>>>(a);
         else flash_fwd_kernel<false, 4><<<grid, 256, 0, st>>>(a);

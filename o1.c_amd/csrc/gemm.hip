@@ -65,211 +65,10 @@ __device__ __forceinline__ float silu_rcp(float g) {
 
 __device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-template <int BM, int BN, int WGM, int WGN, int EPI>
-struct GemmCfg {
-    static constexpr int NW = WGM * WGN;
-    static constexpr int NT = NW * 64;
-    static constexpr int WTM = BM / WGM, WTN = BN / WGN;
-    static constexpr int TM = WTM / 32, TN = WTN / 32;
-    static constexpr int WTN_OUT = EPI == EPI_SWIGLU ? WTN / 2 : WTN;
-    static constexpr int BN_OUT = EPI == EPI_SWIGLU ? BN / 2 : BN;
-    static constexpr int EPAD = 8;   // staging row padding (elements)
-    static constexpr int MAIN_BYTES = 2 * (BM + BN) * 64 * 2;
-    static constexpr int EPI_BYTES = NW * WTM * (WTN_OUT + EPAD) * 2;
-    static constexpr int LDS_BYTES = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
-    static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "loader split");
-    static_assert(TM >= 1 && TN >= 1, "wave tile");
-    static_assert(EPI != EPI_SWIGLU || TN % 2 == 0, "swiglu pairs");
-};
-
 __device__ __forceinline__ int xcd_remap(int b, int nb) {
     const int per = nb / 8, rem = nb % 8;
     const int xcd = b % 8, idx = b / 8;
     return xcd * per + (xcd < rem ? xcd : rem) + idx;
-}
-
-template <int BM, int BN, int WGM, int WGN, int EPI, int PF = 0, int GROUP_M = 8, int SWZ = 0,
-          int DIAG = 0>
-__global__ __launch_bounds__(WGM * WGN * 64) void gemm_bf16_kernel(GemmArgs g) {
-    using Cfg = GemmCfg<BM, BN, WGM, WGN, EPI>;
-    constexpr int NW = Cfg::NW, WTM = Cfg::WTM, WTN = Cfg::WTN, TM = Cfg::TM, TN = Cfg::TN;
-    __shared__ __attribute__((aligned(1024))) uint16_t smem[Cfg::LDS_BYTES / 2];
-
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave / WGN, wn = wave % WGN;
-
-    // ---- tile coordinates: XCD-contiguous, grouped raster ----------------
-    const int nblk = g.ntm * g.ntn;
-    const int lin = xcd_remap(blockIdx.x, nblk);
-    const int in_group = GROUP_M * g.ntn;
-    const int first_m = (lin / in_group) * GROUP_M;
-    const int gm = min(g.ntm - first_m, GROUP_M);
-    const int tm = first_m + (lin % in_group) % gm;
-    const int tn = (lin % in_group) / gm;
-    const int m0 = tm * BM;
-
-    // ---- per-lane source rows of the loader (constant over K) ------------
-    constexpr int AI = BM / 8 / NW, BI = BN / 8 / NW;
-    const uint16_t *a_src[AI];
-    const uint16_t *b_src[BI];
-    // LDS slot (row, s) holds 16-byte chunk s ^ swz(row) of the row, so the
-    // fragment reads of 16 consecutive rows spread over all banks.
-    auto swz = [](int r) { return SWZ ? ((r >> 1) & 7) : (r & 7); };
-    const int sub = lane >> 3;                  // row within an 8-row group
-#pragma unroll
-    for (int i = 0; i < AI; i++) {
-        int r = (wave * AI + i) * 8 + sub;
-        int m = min(m0 + r, g.M - 1);
-        a_src[i] = g.A + (size_t)m * g.K + ((lane & 7) ^ swz(r)) * 8;
-    }
-#pragma unroll
-    for (int i = 0; i < BI; i++) {
-        int r = (wave * BI + i) * 8 + sub;
-        const int chunk = (lane & 7) ^ swz(r);
-        const uint16_t *p;
-        if (EPI == EPI_SWIGLU) {
-            int grp = r / WTN, j = r % WTN;
-            int n = tn * Cfg::BN_OUT + grp * (WTN / 2) + (j % (WTN / 2));
-            n = min(n, g.N - 1);
-            p = (j < WTN / 2 ? g.B[0] : g.B[1]) + (size_t)n * g.K;
-        } else {
-            int n = min(tn * BN + r, g.seg_end[2] - 1);
-            int s = n < g.seg_end[0] ? 0 : (n < g.seg_end[1] ? 1 : 2);
-            int base = s == 0 ? 0 : g.seg_end[s - 1];
-            p = g.B[s] + (size_t)(n - base) * g.K;
-        }
-        b_src[i] = p + chunk * 8;
-    }
-
-    uint16_t *As0 = smem, *Bs0 = smem + 2 * BM * 64;
-    auto issue = [&](int kt, int buf) {
-        uint16_t *As = As0 + buf * BM * 64, *Bs = Bs0 + buf * BN * 64;
-#pragma unroll
-        for (int i = 0; i < AI; i++)
-            __builtin_amdgcn_global_load_lds((const void *)(a_src[i] + kt * 64),
-                                             (HD_LDS void *)(As + (wave * AI + i) * 512), 16, 0, 0);
-#pragma unroll
-        for (int i = 0; i < BI; i++)
-            __builtin_amdgcn_global_load_lds((const void *)(b_src[i] + kt * 64),
-                                             (HD_LDS void *)(Bs + (wave * BI + i) * 512), 16, 0, 0);
-    };
-
-    f32x16_t acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
-
-    const int nk = g.K / 64;
-    const int l32 = lane & 31, khalf = lane >> 5;
-    const int sw = SWZ ? ((l32 >> 1) & 7) : (lane & 7);   // swz(row): row = 32*t + l32
-    issue(0, 0);
-    wait_vm0();
-    __syncthreads();
-    for (int kt = 0; kt < nk; kt++) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk && DIAG != 1) issue(kt + 1, buf ^ 1);   // DIAG 1: compute only
-        const uint16_t *As = As0 + buf * BM * 64, *Bs = Bs0 + buf * BN * 64;
-        if (DIAG == 2) {
-            // load-only diagnostic: one fragment read, no MFMA
-            acc[0][0][0] += (float)(*(const bf16x8_t *)(As + l32 * 64))[0];
-        } else if (PF) {
-            // fragments of k-step ks+1 are read while the MFMAs of ks run
-            bf16x8_t af[2][TM], bw[2][TN];
-            auto ld = [&](int ks, int slot) {
-                const int c = ((ks * 2 + khalf) ^ sw) * 8;
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-                    af[slot][i] = *(const bf16x8_t *)(As + (wm * WTM + i * 32 + l32) * 64 + c);
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    bw[slot][j] = *(const bf16x8_t *)(Bs + (wn * WTN + j * 32 + l32) * 64 + c);
-            };
-            ld(0, 0);
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                if (ks < 3) ld(ks + 1, (ks + 1) & 1);
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int j = 0; j < TN; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[ks & 1][j], af[ks & 1][i],
-                                                                             acc[i][j], 0, 0, 0);
-            }
-        } else {
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            const int c = ((ks * 2 + khalf) ^ sw) * 8;
-            bf16x8_t af[TM], bw[TN];
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-                af[i] = *(const bf16x8_t *)(As + (wm * WTM + i * 32 + l32) * 64 + c);
-#pragma unroll
-            for (int j = 0; j < TN; j++)
-                bw[j] = *(const bf16x8_t *)(Bs + (wn * WTN + j * 32 + l32) * 64 + c);
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[j], af[i], acc[i][j], 0, 0, 0);
-        }
-        }
-        wait_vm0();
-        __syncthreads();
-    }
-
-    // ---- epilogue: stage bf16 through LDS, write coalesced rows ----------
-    constexpr int WO = Cfg::WTN_OUT, LDW = WO + Cfg::EPAD;
-    uint16_t *stg = smem + wave * WTM * LDW;
-#pragma unroll
-    for (int i = 0; i < TM; i++) {
-        const int row = i * 32 + l32;
-#pragma unroll
-        for (int j = 0; j < (EPI == EPI_SWIGLU ? TN / 2 : TN); j++) {
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                float v[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    float x = acc[i][j][q * 4 + e];
-                    if (EPI == EPI_SWIGLU) {
-                        float gt = bfround(x);
-                        float up = bfround(acc[i][j + TN / 2][q * 4 + e]);
-                        float sg = bfround(silu_rcp(gt));
-                        x = sg * up;
-                    }
-                    v[e] = x;
-                }
-                const int col = j * 32 + q * 8 + khalf * 4;
-                u32x2_t pk = {pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
-                *(u32x2_t *)(stg + row * LDW + col) = pk;
-            }
-        }
-    }
-    __syncthreads();
-    constexpr int CPR = WO / 8;              // 16-byte chunks per staged row
-    constexpr int RPI = 64 / CPR;            // rows per wave instruction
-    const int gm0 = m0 + wm * WTM;
-    const int gn0 = tn * Cfg::BN_OUT + wn * WO;
-#pragma unroll 4
-    for (int r0 = 0; r0 < WTM; r0 += RPI) {
-        const int r = r0 + lane / CPR, cc = (lane % CPR) * 8;
-        const int m = gm0 + r, n = gn0 + cc;
-        if (m < g.M && n < g.N) {
-            u32x4_t v = *(const u32x4_t *)(stg + r * LDW + cc);
-            if (EPI == EPI_BIAS || EPI == EPI_RES) {
-                u32x4_t o = EPI == EPI_BIAS ? *(const u32x4_t *)(g.bias + n)
-                                            : *(const u32x4_t *)(g.res + (size_t)m * g.ldc + n);
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    v[e] = pack_bf2(lo_bf(v[e]) + lo_bf(o[e]), hi_bf(v[e]) + hi_bf(o[e]));
-            }
-            *(u32x4_t *)(g.C + (size_t)m * g.ldc + n) = v;
-        }
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -459,17 +258,27 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs &g, uint16_t *stg, i
     }
 }
 
-template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 0, int OCC = 1,
-          int LDR = 0, int MF = 32>
+// Production GEMM kernel. Template arguments: block tile BM x BN x BK, NS
+// LDS stages, WGM x WGN waves, epilogue EPI, schedule SGB, blocks per CU OCC,
+// loader LDR, MFMA shape MF (16: v_mfma_f32_16x16x32_bf16).
+//   SGB 8, LDR 5: split operand rings (A three stages, B two; 160 KB for
+//     256 x 256 tiles) filled by buffer loads straight to LDS (operands under
+//     2 GiB: 32-bit byte offsets), the next k-step's fragment reads and a
+//     tile's refill loads placed between every other MFMA;
+//   SGB 3, LDR 0: equal-depth rings filled by global_load_lds (64-bit
+//     addresses), for operands of 2 GiB or more.
+// Both keep one fragment ring across the whole K loop: the fragments of
+// k-step ks+1 load under the MFMAs of ks, and at the last k-step of a tile
+// the barrier, the refill of the freed stage and the first fragments of the
+// next tile all go under that k-step's MFMAs.
+template <int BM, int BN, int BK, int NS, int WGM, int WGN, int EPI, int SGB = 8, int OCC = 1,
+          int LDR = 5, int MF = 16>
 __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g) {
-    // MF: MFMA shape, 32 (v_mfma_f32_32x32x16_bf16) or 16 (16x16x32, SGB 3 only)
-    constexpr bool SPLITR = SGB == 4 || SGB == 5 || SGB >= 8;
-    static_assert(MF == 32 || SGB == 3 || SGB == 4 || SGB >= 8, "16x16 MFMA tiles: fragment-ring schedules");
-    static_assert(!SPLITR || (LDR == 5 && NS == 2), "split rings: buffer loads, 2+1 stages");
-    constexpr bool BDEEP = SGB == 5 || SGB == 11;
-    using C = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI, MF, SPLITR && !BDEEP ? 1 : 0, BDEEP ? 1 : 0>;
-    using AccT = typename std::conditional<MF == 32, f32x16_t, f32x4_t>::type;
-    constexpr int ACCN = MF == 32 ? 16 : 4;
+    static_assert(MF == 16 && BK == 64 && NS == 2, "16x16x32 MFMA tiles, 64-deep K tiles, 2+ stages");
+    static_assert((SGB == 8 && LDR == 5) || (SGB == 3 && LDR == 0), "schedule / loader pair");
+    constexpr bool SPLITR = SGB == 8;
+    using C = MsCfg<BM, BN, BK, NS, WGM, WGN, EPI, MF, SPLITR ? 1 : 0, 0>;
+    using AccT = f32x4_t;
     constexpr int WTM = C::WTM, WTN = C::WTN, TM = C::TM, TN = C::TN, CPR = C::CPR;
     constexpr int AI = C::AI, BI = C::BI, GROUP_M = 8;
     __shared__ __attribute__((aligned(1024))) uint16_t smem[C::LDS_BYTES / 2];
@@ -501,115 +310,63 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
         nk = k1 - k0;
     }
 
-    const uint16_t *a_src[AI];
-    const uint16_t *b_src[BI];
     const int sub = lane / CPR, cl = lane % CPR;
-#pragma unroll
-    for (int i = 0; i < AI; i++) {
-        int r = (wave * AI + i) * C::RPI + sub;
-        int m = min(m0 + r, g.M - 1);
-        a_src[i] = g.A + (size_t)m * g.K + (cl ^ ms_swz<CPR>(r)) * 8;
-    }
-#pragma unroll
-    for (int i = 0; i < BI; i++) {
-        int r = (wave * BI + i) * C::RPI + sub;
-        const uint16_t *p;
-        if (EPI == EPI_SWIGLU) {
-            int grp = r / WTN, j = r % WTN;
-            int n = tn * C::BN_OUT + grp * (WTN / 2) + (j % (WTN / 2));
-            n = min(n, g.N - 1);
-            p = (j < WTN / 2 ? g.B[0] : g.B[1]) + (size_t)n * g.K;
-        } else {
-            // a 256-aligned column tile lies in one weight segment (q/k/v)
-            const int t0 = tn * BN;
-            const int sg = t0 < g.seg_end[0] ? 0 : (t0 < g.seg_end[1] ? 1 : 2);
-            const uint16_t *bp = sg == 0 ? g.B[0] : (sg == 1 ? g.B[1] : g.B[2]);
-            const int base = sg == 0 ? 0 : (sg == 1 ? g.seg_end[0] : g.seg_end[1]);
-            const int last = (sg == 0 ? g.seg_end[0] : (sg == 1 ? g.seg_end[1] : g.seg_end[2])) - 1;
-            int n = min(t0 + r, last);
-            p = bp + (size_t)(n - base) * g.K;
-        }
-        b_src[i] = p + (cl ^ ms_swz<CPR>(r)) * 8;
-    }
-    // LDR 2 (diagnostic): every K tile re-reads tile 0, so all loads hit in
-    // cache and the instruction stream is otherwise unchanged
-    auto koff = [&](int kt) { return LDR == 2 ? 0 : (kbase + kt) * BK; };
-    // LDR 5: buffer loads straight to LDS (MUBUF: 32-bit per-lane byte
-    // offsets against a scalar descriptor; the K advance is the scalar
-    // offset; rows past the matrix read as zero through the record limit)
-    // segment of this column tile (QKV) / the gate and up matrices (SwiGLU)
+    // segment of this column tile (QKV: a 256-aligned column tile lies in one
+    // of the q/k/v weights) or the gate and up matrices (SwiGLU)
     const int bt0 = tn * BN;
     const int bsg = EPI == EPI_SWIGLU ? 0 : (bt0 < g.seg_end[0] ? 0 : (bt0 < g.seg_end[1] ? 1 : 2));
     const int bbase = bsg == 0 ? 0 : (bsg == 1 ? g.seg_end[0] : g.seg_end[1]);
     const int brows = EPI == EPI_SWIGLU ? g.N
                                         : (bsg == 0 ? g.seg_end[0] : (bsg == 1 ? g.seg_end[1] : g.seg_end[2])) - bbase;
     const void *bp_a = g.A, *bp_b0 = bsg == 0 ? g.B[0] : (bsg == 1 ? g.B[1] : g.B[2]), *bp_b1 = g.B[1];
+    // B row r of the tile -> weight row n (SwiGLU: each wave's WTN rows are
+    // WTN/2 gate rows then the up rows of the same output columns), and
+    // which matrix it comes from
+    auto b_row = [&](int r, int &rs) {
+        if (EPI == EPI_SWIGLU) {
+            const int grp = r / WTN, j = r % WTN;
+            rs = j < WTN / 2 ? 0 : 1;
+            return tn * C::BN_OUT + grp * (WTN / 2) + (j % (WTN / 2));
+        }
+        rs = 0;
+        return bt0 + r - bbase;
+    };
+    // LDR 0: 64-bit source pointers per loader row (global_load_lds)
+    const uint16_t *a_src[AI];
+    const uint16_t *b_src[BI];
+    // LDR 5: 32-bit per-lane byte offsets against a scalar descriptor; the K
+    // advance is the scalar offset; rows past the matrix read as zero
+    // through the record limit
     const int nb_a = (int)((size_t)g.M * g.K * 2), nb_b = (int)((size_t)brows * g.K * 2);
     uint32_t a_vo[AI], b_vo[BI];
     int b_rs[BI];
-    if constexpr (LDR == 5 || LDR == 6) {
 #pragma unroll
-        for (int i = 0; i < AI; i++) {
-            const int r = (wave * AI + i) * C::RPI + sub;
+    for (int i = 0; i < AI; i++) {
+        const int r = (wave * AI + i) * C::RPI + sub;
+        if constexpr (LDR == 5) {
             a_vo[i] = ((uint32_t)(m0 + r) * (uint32_t)g.K + (uint32_t)(cl ^ ms_swz<CPR>(r)) * 8) * 2;
-        }
-#pragma unroll
-        for (int i = 0; i < BI; i++) {
-            const int r = (wave * BI + i) * C::RPI + sub;
-            int n;
-            if (EPI == EPI_SWIGLU) {
-                const int grp = r / WTN, j = r % WTN;
-                n = tn * C::BN_OUT + grp * (WTN / 2) + (j % (WTN / 2));
-                // the RPI rows of one load share a side of the gate/up split:
-                // decide it from the wave-uniform first row
-                b_rs[i] = (((wave * BI + i) * C::RPI) % WTN) < WTN / 2 ? 0 : 1;
-            } else {
-                n = bt0 + r - bbase;
-                b_rs[i] = 0;
-            }
-            b_vo[i] = n >= brows ? 0x80000000u   // past the records (< 2^31): reads zero
-                                 : ((uint32_t)n * (uint32_t)g.K + (uint32_t)(cl ^ ms_swz<CPR>(r)) * 8) * 2;
+        } else {
+            const int m = min(m0 + r, g.M - 1);
+            a_src[i] = g.A + (size_t)m * g.K + (cl ^ ms_swz<CPR>(r)) * 8;
         }
     }
-    auto issue = [&](int kt, int st) {
-        if (LDR == 3) return;   // diagnostic: no global->LDS traffic
-        uint16_t *As = smem + st * C::STAGE, *Bs = As + BM * BK;
-        if constexpr (LDR == 5 || LDR == 6) {
-            const uint32_t so = (uint32_t)(kbase + kt) * BK * 2;
 #pragma unroll
-            for (int i = 0; i < AI; i++)
-                buf_load_lds16(bp_a, nb_a, a_vo[i], so, (HD_LDS void *)(As + (wave * AI + i) * 512));
-#pragma unroll
-            for (int i = 0; i < BI; i++)
-                buf_load_lds16(b_rs[i] ? bp_b1 : bp_b0, nb_b, b_vo[i], so,
-                               (HD_LDS void *)(Bs + (wave * BI + i) * 512));
-            return;
+    for (int i = 0; i < BI; i++) {
+        const int r = (wave * BI + i) * C::RPI + sub;
+        int rs, rs0;
+        const int n = b_row(r, rs);
+        // the RPI rows of one load share a side of the gate/up split: take it
+        // from the wave-uniform first row, so the descriptor stays scalar
+        (void)b_row((wave * BI + i) * C::RPI, rs0);
+        b_rs[i] = rs0;
+        if constexpr (LDR == 5) {
+            b_vo[i] = n >= brows ? 0x80000000u   // past the records (< 2^31): reads zero
+                                 : ((uint32_t)n * (uint32_t)g.K + (uint32_t)(cl ^ ms_swz<CPR>(r)) * 8) * 2;
+        } else {
+            const int nn = min(n, brows - 1);
+            b_src[i] = (const uint16_t *)(rs ? bp_b1 : bp_b0) + (size_t)nn * g.K + (cl ^ ms_swz<CPR>(r)) * 8;
         }
-#pragma unroll
-        for (int i = 0; i < AI; i++)
-            __builtin_amdgcn_global_load_lds((const void *)(a_src[i] + koff(kt)),
-                                             (HD_LDS void *)(As + (wave * AI + i) * 512), 16, 0, 0);
-#pragma unroll
-        for (int i = 0; i < BI; i++)
-            __builtin_amdgcn_global_load_lds((const void *)(b_src[i] + koff(kt)),
-                                             (HD_LDS void *)(Bs + (wave * BI + i) * 512), 16, 0, 0);
-    };
-    // LDR 1: the same chunks through registers (global_load_dwordx4 then
-    // ds_write_b128 at the swizzled slot), each lane keeping its rows.
-    u32x4_t ra[AI], rb[BI];
-    auto gload = [&](int kt) {
-#pragma unroll
-        for (int i = 0; i < AI; i++) ra[i] = *(const u32x4_t *)(a_src[i] + (kbase + kt) * BK);
-#pragma unroll
-        for (int i = 0; i < BI; i++) rb[i] = *(const u32x4_t *)(b_src[i] + (kbase + kt) * BK);
-    };
-    auto lstore = [&](int st) {
-        uint16_t *As = smem + st * C::STAGE, *Bs = As + BM * BK;
-#pragma unroll
-        for (int i = 0; i < AI; i++) *(u32x4_t *)(As + (wave * AI + i) * 512 + lane * 8) = ra[i];
-#pragma unroll
-        for (int i = 0; i < BI; i++) *(u32x4_t *)(Bs + (wave * BI + i) * 512 + lane * 8) = rb[i];
-    };
+    }
 
     AccT acc[TM][TN];
 #pragma unroll
@@ -617,25 +374,35 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
 #pragma unroll
         for (int j = 0; j < TN; j++)
 #pragma unroll
-            for (int r = 0; r < ACCN; r++) acc[i][j][r] = 0.f;
+            for (int r = 0; r < 4; r++) acc[i][j][r] = 0.f;
 
-    const int l32 = lane & 31, khalf = lane >> 5;
-    const int sw = ms_swz<CPR>(l32);
+    // k-steps of 32 per 64-deep tile; a lane reads 8 consecutive k of row
+    // lane % 16, chunk lane / 16 of the step
+    constexpr int KS = BK / 32, CPS = 4, NR = TM + TN, NM = TM * TN;
+    static_assert(KS % 2 == 0, "fragment slots");
+    const int lr = lane % MF, lc = lane / MF, swr = ms_swz<CPR>(lr);
+    bf16x8_t af[2][TM], bw[2][TN];
+    auto mfmas = [&](int sl) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bw[sl][j], af[sl][i], acc[i][j], 0, 0, 0);
+    };
     if constexpr (SGB == 3) {
-        // One fragment ring across the whole K loop (one wave per SIMD has no
-        // partner wave to cover a refill bubble): the fragments of k-step
-        // ks+1 load under the MFMAs of ks, and at the last k-step of a tile
-        // the barrier, the refill of the stage just read and the first
-        // fragments of the next tile all go under that k-step's MFMAs.
-        // k-steps per tile: 16 deep (32x32x16) or 32 deep (16x16x32); a lane
-        // reads 8 consecutive k of row lane % MF, chunk lane / MF of the step
-        constexpr int KS = BK / (MF == 32 ? 16 : 32), NR = TM + TN, NM = TM * TN, LPT = C::LPT;
-        constexpr int CPS = 64 / MF;   // 16-byte chunks per k-step
-        static_assert(KS % 2 == 0, "fragment slots");
-        const int lr = lane % MF, lc = lane / MF, swr = ms_swz<CPR>(lr);
-        bf16x8_t af[2][TM], bw[2][TN];
+        constexpr int LPT = C::LPT;
+        auto issue = [&](int kt, int st) {
+            uint16_t *As = smem + st * C::STAGE, *Bs = As + BM * BK;
+#pragma unroll
+            for (int i = 0; i < AI; i++)
+                __builtin_amdgcn_global_load_lds((const void *)(a_src[i] + (kbase + kt) * BK),
+                                                 (HD_LDS void *)(As + (wave * AI + i) * 512), 16, 0, 0);
+#pragma unroll
+            for (int i = 0; i < BI; i++)
+                __builtin_amdgcn_global_load_lds((const void *)(b_src[i] + (kbase + kt) * BK),
+                                                 (HD_LDS void *)(Bs + (wave * BI + i) * 512), 16, 0, 0);
+        };
         auto ld = [&](const uint16_t *As, int ks, int sl) {
-            if (LDR == 4 && ks + 1 > 0 && sl >= 0 && As != smem) return;   // diagnostic: no fragment reads
             const uint16_t *Bs = As + BM * BK;
             const int c = ((ks * CPS + lc) ^ swr) * 8;
 #pragma unroll
@@ -671,17 +438,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
                     if (REFILL) issue(kt + NS, kt % NS);
                     if (NEXT) ld(smem + ((kt + 1) % NS) * C::STAGE, 0, 0);
                 }
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int j = 0; j < TN; j++) {
-                        if constexpr (MF == 32)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[ks & 1][j], af[ks & 1][i],
-                                                                                 acc[i][j], 0, 0, 0);
-                        else
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bw[ks & 1][j], af[ks & 1][i],
-                                                                                 acc[i][j], 0, 0, 0);
-                    }
+                mfmas(ks & 1);
                 const int nv = last && REFILL ? LPT : 0;
                 const int nr = !last || NEXT ? NR : 0;
 #pragma unroll
@@ -698,31 +455,15 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
         for (; kt + NS < nk; kt++) tile(kt, T_{}, T_{});
         for (; kt + 1 < nk; kt++) tile(kt, F_{}, T_{});
         tile(kt, F_{}, F_{});
-    } else if constexpr (SPLITR) {
-        // The fragment ring of schedule 3 with split operand rings in the
-        // 160 KB of LDS: one operand three stages deep, the other two
-        // (schedule 4: A deep - the activation rows, shared by fewer of an
-        // XCD's concurrent tiles, so more of their slices miss L2; schedule
-        // 5: B deep). Each refill batch issues the shallow operand's tile
-        // kt+2 before the deep operand's tile kt+3, so the wait at the end of
-        // tile kt (both operands of tile kt+1 landed) may leave the newest
-        // deep loads in flight: the deep operand gets two tiles of latency,
-        // the other one.
-        constexpr bool DA = !BDEEP;
-        // SGB 8-10: the fragment reads / refill loads go between every SPR-th
-        // / SPV-th MFMA
-        constexpr int SPR = SGB == 8 || SGB == 9 || SGB == 11 ? 2 : 1,
-                      SPV = SGB == 8 || SGB == 11 ? 2 : (SGB == 9 || SGB == 10 ? 4 : 1);
-        // k-steps per tile: 16 deep (32x32x16) or 32 deep (16x16x32); a lane
-        // reads 8 consecutive k of row lane % MF, chunk lane / MF of the step
-        constexpr int KS = BK / (MF == 32 ? 16 : 32), CPS = 64 / MF;
-        constexpr int NR = TM + TN, NM = TM * TN, AI_ = C::AI, BI_ = C::BI;
-        constexpr int NSA = NS + (DA ? 1 : 0), NSB = NS + (DA ? 0 : 1), ASTG = BM * BK, BSTG = BN * BK;
-        constexpr int ND = DA ? AI_ : BI_, NSH = DA ? BI_ : AI_;   // loads per batch: deep, shallow
-        static_assert(KS % 2 == 0, "fragment slots");
+    } else {
+        // Split operand rings in the 160 KB of LDS: A (the activation rows,
+        // shared by fewer of an XCD's concurrent tiles than the weight rows,
+        // so more of their slices miss L2) three stages deep, B two. Each
+        // refill batch issues B's tile kt+2 before A's tile kt+3, so the wait
+        // at the end of tile kt (both operands of tile kt+1 landed) may leave
+        // the newest A loads in flight: A gets two tiles of latency, B one.
+        constexpr int NSA = NS + 1, NSB = NS, ASTG = BM * BK, BSTG = BN * BK;
         uint16_t *const Abase = smem, *const Bbase = smem + NSA * ASTG;
-        const int lr = lane % MF, lc = lane / MF, swr = ms_swz<CPR>(lr);
-        bf16x8_t af[2][TM], bw[2][TN];
         auto ld = [&](int kt, int ks, int sl) {
             const uint16_t *As = Abase + (kt % NSA) * ASTG, *Bs = Bbase + (kt % NSB) * BSTG;
             const int c = ((ks * CPS + lc) ^ swr) * 8;
@@ -737,42 +478,34 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
             uint16_t *As = Abase + (kt % NSA) * ASTG;
             const uint32_t so = (uint32_t)(kbase + kt) * BK * 2;
 #pragma unroll
-            for (int i = 0; i < AI_; i++)
-                buf_load_lds16(bp_a, nb_a, a_vo[i], so, (HD_LDS void *)(As + (wave * AI_ + i) * 512));
+            for (int i = 0; i < AI; i++)
+                buf_load_lds16(bp_a, nb_a, a_vo[i], so, (HD_LDS void *)(As + (wave * AI + i) * 512));
         };
         auto issue_b = [&](int kt) {
             uint16_t *Bs = Bbase + (kt % NSB) * BSTG;
             const uint32_t so = (uint32_t)(kbase + kt) * BK * 2;
 #pragma unroll
-            for (int i = 0; i < BI_; i++)
+            for (int i = 0; i < BI; i++)
                 buf_load_lds16(b_rs[i] ? bp_b1 : bp_b0, nb_b, b_vo[i], so,
-                               (HD_LDS void *)(Bs + (wave * BI_ + i) * 512));
+                               (HD_LDS void *)(Bs + (wave * BI + i) * 512));
         };
-        auto issue_deep = [&](int kt) {
-            if constexpr (DA) issue_a(kt);
-            else issue_b(kt);
-        };
-        auto issue_shallow = [&](int kt) {
-            if constexpr (DA) issue_b(kt);
-            else issue_a(kt);
-        };
-        // prologue: [S0 D0] [S1 D1] [D2]; tile 0 may leave the later ones in flight
-        issue_shallow(0);
-        issue_deep(0);
+        // prologue: [B0 A0] [B1 A1] [A2]; tile 0 may leave the later ones in flight
+        issue_b(0);
+        issue_a(0);
         if (nk >= 2) {
-            issue_shallow(1);
-            issue_deep(1);
+            issue_b(1);
+            issue_a(1);
         }
         if (nk >= 3) {
-            issue_deep(2);
-            wait_vm_barrier<NSH + 2 * ND>();
+            issue_a(2);
+            wait_vm_barrier<BI + 2 * AI>();
         } else if (nk == 2) {
-            wait_vm_barrier<NSH + ND>();
+            wait_vm_barrier<BI + AI>();
         } else {
             wait_vm_barrier<0>();
         }
         ld(0, 0, 0);
-        // RD: deep tile kt+3 exists, RS: shallow tile kt+2 exists, NX: tile kt+1 exists
+        // RD: A tile kt+3 exists, RS: B tile kt+2 exists, NX: tile kt+1 exists
         auto tile = [&](int kt, auto rd, auto rs, auto nx) {
             constexpr bool RD = decltype(rd)::value, RS = decltype(rs)::value, NX = decltype(nx)::value;
 #pragma unroll
@@ -781,34 +514,25 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
                 if (!last) {
                     ld(kt, ks + 1, (ks + 1) & 1);
                 } else {
-                    // both operands of tile kt+1 have landed (the deep
-                    // operand's tile kt+2, issued after them, may still fly)
-                    // and every wave is done reading the stages of tile kt
-                    if (RS) wait_lgk_vm_barrier<ND>();
+                    // both operands of tile kt+1 have landed (A's tile kt+2,
+                    // issued after them, may still fly) and every wave is
+                    // done reading the stages of tile kt
+                    if (RS) wait_lgk_vm_barrier<AI>();
                     else wait_lgk_vm_barrier<0>();
                     __builtin_amdgcn_sched_barrier(0);
-                    if (RS) issue_shallow(kt + 2);
-                    if (RD) issue_deep(kt + 3);
+                    if (RS) issue_b(kt + 2);
+                    if (RD) issue_a(kt + 3);
                     if (NX) ld(kt + 1, 0, 0);
                 }
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int j = 0; j < TN; j++) {
-                        if constexpr (MF == 32)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[ks & 1][j], af[ks & 1][i],
-                                                                                 acc[i][j], 0, 0, 0);
-                        else
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bw[ks & 1][j], af[ks & 1][i],
-                                                                                 acc[i][j], 0, 0, 0);
-                    }
-                const int nv = last ? (RD ? ND : 0) + (RS ? NSH : 0) : 0;
+                mfmas(ks & 1);
+                // fragment reads and refill loads between every other MFMA
+                const int nv = last ? (RD ? AI : 0) + (RS ? BI : 0) : 0;
                 const int nr = !last || NX ? NR : 0;
 #pragma unroll
                 for (int q = 0; q < NM; q++) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    if (q % SPV == 0 && q / SPV < nv) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-                    if (q % SPR == SPR - 1 && q / SPR < nr) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    if (q % 2 == 0 && q / 2 < nv) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                    if (q % 2 == 1 && q / 2 < nr) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 }
             }
         };
@@ -819,126 +543,21 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
         if (kt + 2 < nk) tile(kt++, F_{}, T_{}, T_{});
         if (kt + 1 < nk) tile(kt++, F_{}, F_{}, T_{});
         tile(kt, F_{}, F_{}, F_{});
-    } else {
-    if (LDR == 1) {
-        // 2-stage ring through registers: load k+1 early, store it after the
-        // MFMAs of k, one barrier per K tile
-        gload(0);
-        lstore(0);
-        __syncthreads();
     }
-    if (LDR != 1) {
+    if (chunk >= 0) {
+        // K chunk of a tail tile: the raw fp32 accumulators, tile-local
+        // [BM][BN] (a lane holds rows i*16 + lane%16, columns j*16 +
+        // (lane/16)*4 .. +3, B-row column order); the merge kernel sums the
+        // chunks and applies the epilogue
+        float *pt = g.part + (size_t)item * BM * BN;
 #pragma unroll
-        for (int s = 0; s < NS - 1; s++)
-            if (s < nk) issue(s, s);
-    }
-    for (int kt = 0; kt < nk; kt++) {
-        if (LDR == 1) {
-            if (kt + 1 < nk) gload(kt + 1);
-        } else {
-            if (kt + NS - 2 < nk) wait_vm_barrier<(NS - 2) * C::LPT>();
-            else wait_vm_barrier<0>();
-            if (kt + NS - 1 < nk) issue(kt + NS - 1, (kt + NS - 1) % NS);
-        }
-        const uint16_t *As = smem + (LDR == 1 ? (kt & 1) : (kt % NS)) * C::STAGE, *Bs = As + BM * BK;
-        if (SGB) {
-            // register double buffer of fragments; the reads of k-step ks+1
-            // are interleaved one by one with the MFMAs of ks (SGB 2: the
-            // tile's global->LDS loads, issued above, are spread between
-            // the MFMAs as well instead of leaving as one burst)
-            bf16x8_t af[2][TM], bw[2][TN];
-            auto ld = [&](int ks, int sl) {
-                const int c = ((ks * 2 + khalf) ^ sw) * 8;
+        for (int i = 0; i < TM; i++)
 #pragma unroll
-                for (int i = 0; i < TM; i++)
-                    af[sl][i] = *(const bf16x8_t *)(As + (wm * WTM + i * 32 + l32) * BK + c);
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    bw[sl][j] = *(const bf16x8_t *)(Bs + (wn * WTN + j * 32 + l32) * BK + c);
-            };
-            ld(0, 0);
-            constexpr int KS = BK / 16, NR = TM + TN, NM = TM * TN;
-            constexpr int NV = SGB == 2 ? (C::LPT + KS - 1) / KS : 0;   // VMEM per k-step
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++) {
-                if (ks + 1 < KS) ld(ks + 1, (ks + 1) & 1);
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int j = 0; j < TN; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[ks & 1][j], af[ks & 1][i],
-                                                                             acc[i][j], 0, 0, 0);
-                const int nr = ks + 1 < KS ? NR : 0;
-                const int nv = NV;
-#pragma unroll
-                for (int q = 0; q < NM; q++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);        // 1 MFMA
-                    if (q < nr) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // 1 DS read
-                    else if (q - nr < nv) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 VMEM
-                }
+            for (int j = 0; j < TN; j++) {
+                const int row = wm * WTM + i * 16 + (lane & 15);
+                const int col = wn * WTN + j * 16 + (lane >> 4) * 4;
+                *(f32x4_t *)(pt + (size_t)row * BN + col) = acc[i][j];
             }
-        } else {
-#pragma unroll
-        for (int ks = 0; ks < BK / 16; ks++) {
-            const int c = ((ks * 2 + khalf) ^ sw) * 8;
-            bf16x8_t af[TM], bw[TN];
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-                af[i] = *(const bf16x8_t *)(As + (wm * WTM + i * 32 + l32) * BK + c);
-#pragma unroll
-            for (int j = 0; j < TN; j++)
-                bw[j] = *(const bf16x8_t *)(Bs + (wn * WTN + j * 32 + l32) * BK + c);
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[j], af[i], acc[i][j], 0, 0, 0);
-        }
-        }
-        if (LDR == 1) {
-            if (kt + 1 < nk) lstore((kt + 1) & 1);
-            __syncthreads();
-        }
-    }
-    }
-    if constexpr (MF == 32) {
-        if (chunk >= 0) {
-            // K chunk of a tail tile: the raw fp32 accumulators, tile-local
-            // [BM][BN] in accumulator column order; the merge kernel sums
-            // the chunks and applies the epilogue
-            float *pt = g.part + (size_t)item * BM * BN;
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        const int row = wm * WTM + i * 32 + l32;
-                        const int col = wn * WTN + j * 32 + q * 8 + khalf * 4;
-                        f32x4_t v = {acc[i][j][q * 4], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2],
-                                     acc[i][j][q * 4 + 3]};
-                        *(f32x4_t *)(pt + (size_t)row * BN + col) = v;
-                    }
-            return;
-        }
-    } else {
-        if (chunk >= 0) {
-            // 16x16 tiles: a lane holds rows i*16 + lane%16, columns
-            // j*16 + (lane/16)*4 .. +3 (tile-local, B-row column order)
-            float *pt = g.part + (size_t)item * BM * BN;
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++) {
-                    const int row = wm * WTM + i * 16 + (lane & 15);
-                    const int col = wn * WTN + j * 16 + (lane >> 4) * 4;
-                    *(f32x4_t *)(pt + (size_t)row * BN + col) = acc[i][j];
-                }
-            return;
-        }
-    }
-    if constexpr (LDR == 6) {   // diagnostic (timing only): no epilogue
-        if (acc[0][0][0] == 12345.f) g.C[threadIdx.x] = 1;   // keeps the K loop live
         return;
     }
     // residual epilogue: this lane's residual chunks are requested before
@@ -964,13 +583,12 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
     constexpr int WO = C::WTN_OUT, LDW = QHALF ? 128 + C::EPAD : WO + C::EPAD;
     uint16_t *const hstg = smem + (wm * (WGN / 2) + wn / 2) * WTM * LDW;   // QHALF: the head's area
     uint16_t *stg = QHALF ? hstg + (wn % 2) * 64 : smem + wave * WTM * LDW;
-    // a lane holds, per accumulator, runs of 4 consecutive output columns:
-    // 32x32: columns q*8 + khalf*4 (q < 4) of row lane % 32;
-    // 16x16: columns (lane / 16)*4 of row lane % 16
-    constexpr int NQ = MF == 32 ? 4 : 1;
+    // a lane holds, per accumulator, 4 consecutive output columns
+    // (lane / 16)*4 .. +3 of row lane % 16
+    constexpr int NQ = 1;
 #pragma unroll
     for (int i = 0; i < TM; i++) {
-        const int row = i * MF + (MF == 32 ? l32 : (lane & 15));
+        const int row = i * MF + (lane & 15);
 #pragma unroll
         for (int j = 0; j < (EPI == EPI_SWIGLU ? TN / 2 : TN); j++) {
 #pragma unroll
@@ -987,7 +605,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
                     }
                     v[e] = x;
                 }
-                const int col = MF == 32 ? j * 32 + q * 8 + khalf * 4 : j * 16 + (lane >> 4) * 4;
+                const int col = j * 16 + (lane >> 4) * 4;
                 u32x2_t pk = {pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
                 *(u32x2_t *)(stg + row * LDW + col) = pk;
             }
@@ -1014,198 +632,6 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
             u32x4_t v = *(const u32x4_t *)(stg + r * LDW + cc);
             if (EPI == EPI_BIAS || EPI == EPI_RES) {
                 u32x4_t o = EPI == EPI_BIAS ? *(const u32x4_t *)(g.bias + n) : resv[EPI == EPI_RES ? r0 / RPIO : 0];
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    v[e] = pack_bf2(lo_bf(v[e]) + lo_bf(o[e]), hi_bf(v[e]) + hi_bf(o[e]));
-            }
-            *(u32x4_t *)(g.C + (size_t)m * g.ldc + n) = v;
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Ping-pong variant: 8 waves in two groups of 4 (one wave of each group per
-// SIMD). Group 0 owns output rows [0, BM/2), group 1 rows [BM/2, BM); each
-// wave a (BM/2) x 64 slice. The groups run one phase apart:
-//   phase 2t   : group 0 reads the fragments of K tile t from LDS into
-//                registers and issues the global->LDS loads of tile t+1;
-//                group 1 runs the MFMAs of tile t-1
-//   phase 2t+1 : group 0 runs the MFMAs of tile t (then waits for tile t+1);
-//                group 1 reads the fragments of tile t
-// with one workgroup barrier between phases, so on every SIMD one wave feeds
-// the matrix core while its partner does memory work. LDS: two 64-deep
-// stages; a stage is rewritten only after both groups have read it.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ void pp_barrier() { asm volatile("s_barrier" ::: "memory"); }
-
-template <int BM, int EPI>
-__global__ __launch_bounds__(512) void gemm_pp_kernel(GemmArgs g) {
-    constexpr int BN = 256, BK = 64, NW = 8;
-    constexpr int WTM = BM / 2, WTN = 64, TM = WTM / 32, TN = 2;
-    constexpr int STAGE = (BM + BN) * BK;
-    constexpr int WTN_OUT = EPI == EPI_SWIGLU ? WTN / 2 : WTN;
-    constexpr int BN_OUT = EPI == EPI_SWIGLU ? BN / 2 : BN;
-    constexpr int EPAD = 8, LDW = WTN_OUT + EPAD;
-    constexpr int MAIN_BYTES = 2 * STAGE * 2, EPI_BYTES = NW * WTM * LDW * 2;
-    constexpr int LDS_BYTES = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
-    constexpr int AI = BM / 8 / 4, BI = BN / 8 / 4;   // loads per group-0 wave
-    constexpr int GROUP_M = 8;
-    __shared__ __attribute__((aligned(1024))) uint16_t smem[LDS_BYTES / 2];
-
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int grp = wave >> 2, wn = wave & 3;
-    const int nblk = g.ntm * g.ntn;
-    const int lin = xcd_remap(blockIdx.x, nblk);
-    const int in_group = GROUP_M * g.ntn;
-    const int first_m = (lin / in_group) * GROUP_M;
-    const int gm = min(g.ntm - first_m, GROUP_M);
-    const int tm = first_m + (lin % in_group) % gm;
-    const int tn = (lin % in_group) / gm;
-    const int m0 = tm * BM;
-
-    // group-0 waves own the global->LDS traffic of whole tiles; the source
-    // addresses are recomputed per tile (cheap in the memory phase, and it
-    // keeps 16 64-bit pointers out of the register budget)
-    const int sub = lane >> 3, cl = lane & 7;
-    const int lw = wave & 3;
-    // weight segments (q/k/v) are multiples of 256 rows: a column tile lies
-    // in one segment, chosen once per block (scalar)
-    const int tile_n0 = __builtin_amdgcn_readfirstlane(tn * BN);
-    const int seg = tile_n0 < g.seg_end[0] ? 0 : (tile_n0 < g.seg_end[1] ? 1 : 2);
-    const uint16_t *seg_ptr = seg == 0 ? g.B[0] : (seg == 1 ? g.B[1] : g.B[2]);
-    const int seg_base = seg == 0 ? 0 : (seg == 1 ? g.seg_end[0] : g.seg_end[1]);
-    const int seg_last = (seg == 0 ? g.seg_end[0] : (seg == 1 ? g.seg_end[1] : g.seg_end[2])) - 1;
-    auto issue = [&](int kt, int st) {
-        uint16_t *As = smem + st * STAGE, *Bs = As + BM * BK;
-        const int k0 = kt * BK;
-#pragma unroll
-        for (int i = 0; i < AI; i++) {
-            const int r = (lw * AI + i) * 8 + sub;
-            const int m = min(m0 + r, g.M - 1);
-            const uint16_t *src = g.A + (size_t)m * g.K + k0 + (cl ^ ms_swz<8>(r)) * 8;
-            __builtin_amdgcn_global_load_lds((const void *)src,
-                                             (HD_LDS void *)(As + (lw * AI + i) * 512), 16, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < BI; i++) {
-            const int r = (lw * BI + i) * 8 + sub;
-            const uint16_t *p;
-            if (EPI == EPI_SWIGLU) {
-                const int gq = r / WTN, j = r % WTN;
-                const int n = min(tn * BN_OUT + gq * (WTN / 2) + (j % (WTN / 2)), g.N - 1);
-                p = (j < WTN / 2 ? g.B[0] : g.B[1]) + (size_t)n * g.K;
-            } else {
-                const int n = min(tn * BN + r, seg_last);
-                p = seg_ptr + (size_t)(n - seg_base) * g.K;
-            }
-            __builtin_amdgcn_global_load_lds((const void *)(p + k0 + (cl ^ ms_swz<8>(r)) * 8),
-                                             (HD_LDS void *)(Bs + (lw * BI + i) * 512), 16, 0, 0);
-        }
-    };
-
-    f32x16_t acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
-
-    const int l32 = lane & 31, khalf = lane >> 5;
-    const int sw = ms_swz<8>(l32);
-    // one phase = half a K tile (2 k-steps): 16 MFMAs, 12 fragment reads
-    bf16x8_t af[2][TM], bw[2][TN];
-    auto frags = [&](int h) {
-        const uint16_t *As = smem + ((h >> 1) & 1) * STAGE, *Bs = As + BM * BK;
-#pragma unroll
-        for (int kk = 0; kk < 2; kk++) {
-            const int ks = (h & 1) * 2 + kk;
-            const int c = ((ks * 2 + khalf) ^ sw) * 8;
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-                af[kk][i] = *(const bf16x8_t *)(As + (grp * WTM + i * 32 + l32) * BK + c);
-#pragma unroll
-            for (int j = 0; j < TN; j++)
-                bw[kk][j] = *(const bf16x8_t *)(Bs + (wn * WTN + j * 32 + l32) * BK + c);
-        }
-    };
-    auto mfmas = [&]() {
-        __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-        for (int kk = 0; kk < 2; kk++)
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[kk][j], af[kk][i], acc[i][j], 0, 0, 0);
-        __builtin_amdgcn_s_setprio(0);
-    };
-
-    const int nk = g.K / BK, NH = 2 * nk;
-    if (grp == 0) {
-        issue(0, 0);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    pp_barrier();
-    // Both groups run the same (memory | barrier | MFMA | barrier) loop over
-    // half tiles; group 1 starts one barrier later and group 0 ends with
-    // one extra, so barrier k pairs group 0's MFMA phase with group 1's
-    // memory phase and vice versa. Group 0 requests K tile t+1 while reading
-    // the first half of tile t and waits for it after its MFMAs on the
-    // second half (four phases of latency).
-    if (grp == 1) pp_barrier();
-    for (int h = 0; h < NH; h++) {
-        const int t = h >> 1;
-        frags(h);
-        if (grp == 0 && (h & 1) == 0 && t + 1 < nk) issue(t + 1, (t + 1) & 1);
-        pp_barrier();
-        mfmas();
-        if (grp == 0 && (h & 1) == 1 && t + 1 < nk) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        pp_barrier();
-    }
-    if (grp == 0) pp_barrier();
-    __syncthreads();
-
-    uint16_t *stg = smem + wave * WTM * LDW;
-#pragma unroll
-    for (int i = 0; i < TM; i++) {
-        const int row = i * 32 + l32;
-#pragma unroll
-        for (int j = 0; j < (EPI == EPI_SWIGLU ? TN / 2 : TN); j++) {
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                float v[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    float x = acc[i][j][q * 4 + e];
-                    if (EPI == EPI_SWIGLU) {
-                        float gt = bfround(x);
-                        float up = bfround(acc[i][j + TN / 2][q * 4 + e]);
-                        float sgm = bfround(silu_rcp(gt));
-                        x = sgm * up;
-                    }
-                    v[e] = x;
-                }
-                const int col = j * 32 + q * 8 + khalf * 4;
-                u32x2_t pk = {pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
-                *(u32x2_t *)(stg + row * LDW + col) = pk;
-            }
-        }
-    }
-    __syncthreads();
-    constexpr int CPRO = WTN_OUT / 8, RPIO = 64 / CPRO;
-    const int gm0 = m0 + grp * WTM;
-    const int gn0 = tn * BN_OUT + wn * WTN_OUT;
-#pragma unroll 4
-    for (int r0 = 0; r0 < WTM; r0 += RPIO) {
-        const int r = r0 + lane / CPRO, cc = (lane % CPRO) * 8;
-        const int m = gm0 + r, n = gn0 + cc;
-        if (m < g.M && n < g.N) {
-            u32x4_t v = *(const u32x4_t *)(stg + r * LDW + cc);
-            if (EPI == EPI_BIAS || EPI == EPI_RES) {
-                u32x4_t o = EPI == EPI_BIAS ? *(const u32x4_t *)(g.bias + n)
-                                            : *(const u32x4_t *)(g.res + (size_t)m * g.ldc + n);
 #pragma unroll
                 for (int e = 0; e < 4; e++)
                     v[e] = pack_bf2(lo_bf(v[e]) + lo_bf(o[e]), hi_bf(v[e]) + hi_bf(o[e]));
@@ -1246,8 +672,7 @@ struct hd_gemm_runtime {
     size_t workspace_bytes;
 };
 static hd_gemm_runtime *g_rt = nullptr;
-static int g_use_production = 1;
-static int g_prod_backend = 0;
+static int g_use_production = 1;   // hd_gemm_set_backend
 
 extern "C" hd_gemm_runtime *hd_gemm_runtime_init(int device_id, size_t workspace_bytes) {
     if (hipSetDevice(device_id) != hipSuccess) {
@@ -1277,16 +702,7 @@ extern "C" void hd_gemm_runtime_destroy(hd_gemm_runtime *rt) {
 extern "C" void *hd_gemm_workspace(hd_gemm_runtime *rt) { return rt ? rt->workspace : nullptr; }
 extern "C" size_t hd_gemm_workspace_bytes(hd_gemm_runtime *rt) { return rt ? rt->workspace_bytes : 0; }
 extern "C" void hd_gemm_set_backend(int p) { g_use_production = p; }
-extern "C" void hd_gemm_set_prod_backend(int b) { g_prod_backend = b; }
-
-template <int BM, int BN, int WGM, int WGN, int EPI, int PF = 0, int GM = 8, int SWZ = 0, int DIAG = 0>
-static void launch_cfg(GemmArgs &g) {
-    using Cfg = GemmCfg<BM, BN, WGM, WGN, EPI>;
-    g.ntm = (g.M + BM - 1) / BM;
-    g.ntn = (g.N + Cfg::BN_OUT - 1) / Cfg::BN_OUT;
-    gemm_bf16_kernel<BM, BN, WGM, WGN, EPI, PF, GM, SWZ, DIAG>
-        <<<g.ntm * g.ntn, Cfg::NT, 0, hd_stream()>>>(g);
-}
+extern "C" void hd_gemm_set_prod_backend(int) {}   // one production family
 
 // Sums the K chunks of each tail tile (fp32, chunk order) and applies the
 // epilogue exactly as gemm_ms_kernel does on its accumulators: four output
@@ -1307,9 +723,7 @@ __global__ void gemm_tail_merge_kernel(GemmArgs g, int n_tail) {
     const int m = tm * BM + r, n = tn * BN_OUT + c;
     if (m >= g.M || n >= g.N) return;
     const int ca = EPI == EPI_SWIGLU ? (c / WO) * WTN + c % WO : c;   // accumulator column
-    // EPI_QKV: bf16 projection of the tail tiles into a tile-local staging
-    // area after the partials; gemm_tail_qkv_epi_kernel finishes them
-    uint16_t *const stage = EPI == EPI_QKV ? (uint16_t *)(g.part + (size_t)n_tail * g.split * BM * BN) : nullptr;
+    static_assert(EPI != EPI_QKV, "QKV tails: gemm_tail_qkv_fused_kernel");
     f32x4_t a = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
     for (int p = 0; p < g.split; p++) {
         const float *pt = g.part + ((size_t)(t * g.split + p) * BM + r) * BN;
@@ -1328,10 +742,6 @@ __global__ void gemm_tail_merge_kernel(GemmArgs g, int n_tail) {
         v[e] = x;
     }
     u32x2_t pk = {pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
-    if (EPI == EPI_QKV) {
-        *(u32x2_t *)(stage + ((size_t)t * BM + r) * BN + c) = pk;
-        return;
-    }
     if (EPI == EPI_BIAS || EPI == EPI_RES) {
         const uint16_t *o = EPI == EPI_BIAS ? g.bias + n : g.res + (size_t)m * g.ldc + n;
         const u32x2_t ov = *(const u32x2_t *)o;
@@ -1339,34 +749,6 @@ __global__ void gemm_tail_merge_kernel(GemmArgs g, int n_tail) {
         for (int e = 0; e < 2; e++) pk[e] = pack_bf2(lo_bf(pk[e]) + lo_bf(ov[e]), hi_bf(pk[e]) + hi_bf(ov[e]));
     }
     *(u32x2_t *)(g.C + (size_t)m * g.ldc + n) = pk;
-}
-
-// EPI_QKV tail tiles, second pass: one wave per (tile, 32-row slice, head)
-// copies its slice of the staged bf16 projection into LDS in the layout
-// gemm_ms_kernel stages it and runs the same qkv_epilogue.
-template <int BM, int BN>
-__global__ __launch_bounds__(64) void gemm_tail_qkv_epi_kernel(GemmArgs g, int n_tail) {
-    constexpr int RS = 32, LDW = 128 + 8, GROUP_M = 8, NSL = BM / RS, NH = BN / 128;
-    __shared__ __attribute__((aligned(16))) uint16_t stg[RS * LDW];
-    const int lane = threadIdx.x;
-    const int b = blockIdx.x;
-    const int hc = b % NH, sl = (b / NH) % NSL, t = b / (NH * NSL);
-    const int lin = g.n_whole + t;
-    const int in_group = GROUP_M * g.ntn;
-    const int first_m = (lin / in_group) * GROUP_M;
-    const int gm = min(g.ntm - first_m, GROUP_M);
-    const int tm = first_m + (lin % in_group) % gm, tn = (lin % in_group) / gm;
-    const uint16_t *src = (const uint16_t *)(g.part + (size_t)n_tail * g.split * BM * BN) +
-                          ((size_t)t * BM + sl * RS) * BN + hc * 128;
-#pragma unroll
-    for (int idx = lane; idx < RS * 16; idx += 64) {
-        const int r = idx / 16, c = (idx % 16) * 8;
-        *(u32x4_t *)(stg + r * LDW + c) = *(const u32x4_t *)(src + (size_t)r * BN + c);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    qkv_epilogue<RS, LDW>(g, stg, tm * BM + sl * RS, (tn * BN) / 128 + hc, lane);
 }
 
 // Rows per wave of the fused QKV tail (32: 22.6 vs 23.6 us with 64 for a
@@ -1468,106 +850,22 @@ static void launch_ms(GemmArgs &g, void *ws = nullptr, int64_t ws_bytes = 0) {
     gemm_ms_kernel<BM, BN, BK, NS, WGM, WGN, EPI, SGB, OCC, LDR, MF>
         <<<(unsigned)(g.n_whole + n_tail * P), Cfg::NT, 0, hd_stream()>>>(g);
     if (n_tail) {
-        if constexpr (EPI == EPI_QKV && BM % QKV_TAIL_RS == 0) {
+        if constexpr (EPI == EPI_QKV) {
+            static_assert(BM % QKV_TAIL_RS == 0, "QKV tail slices");
             gemm_tail_qkv_fused_kernel<BM, BN, QKV_TAIL_RS>
                 <<<(unsigned)(n_tail * (BM / QKV_TAIL_RS) * (BN / 128)), 64, 0, hd_stream()>>>(g, (int)n_tail);
         } else {
             gemm_tail_merge_kernel<BM, BN, WGN, EPI>
                 <<<hd_cdiv((size_t)n_tail * BM * (Cfg::BN_OUT / 4), 256), 256, 0, hd_stream()>>>(
                     g, (int)n_tail);
-            if constexpr (EPI == EPI_QKV)
-                gemm_tail_qkv_epi_kernel<BM, BN>
-                    <<<(unsigned)(n_tail * (BM / 32) * (BN / 128)), 64, 0, hd_stream()>>>(g, (int)n_tail);
         }
-    }
-}
-
-template <int BM, int EPI>
-static void launch_pp(GemmArgs &g) {
-    g.ntm = (g.M + BM - 1) / BM;
-    g.ntn = (g.N + (EPI == EPI_SWIGLU ? 128 : 256) - 1) / (EPI == EPI_SWIGLU ? 128 : 256);
-    gemm_pp_kernel<BM, EPI><<<g.ntm * g.ntn, 512, 0, hd_stream()>>>(g);
-}
-
-// Tuning table: every configuration that hd_gemm_tune_run can launch.
-template <int EPI>
-static bool run_table(int cfg, GemmArgs &g) {
-    switch (cfg) {
-    case 0: launch_cfg<256, 256, 2, 2, EPI, 0, 8, 1>(g); return true;       // 4 waves, 2 stages
-    case 1: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1>(g); return true;       // 8 waves
-    case 2: launch_cfg<128, 128, 2, 2, EPI>(g); return true;
-    case 3: launch_ms<256, 256, 64, 2, 2, 4, EPI, 1>(g); return true;      // production, main
-    case 4: launch_ms<192, 256, 64, 2, 2, 4, EPI, 1>(g); return true;      // production, 192 rows
-    case 5: launch_ms<192, 256, 64, 2, 2, 4, EPI>(g); return true;
-    case 6: launch_ms<256, 256, 32, 4, 2, 4, EPI, 1>(g); return true;      // 4-stage ring
-    case 9: launch_ms<256, 256, 64, 2, 2, 4, EPI, 2>(g); return true;      // loads spread
-    case 10: launch_ms<256, 256, 32, 4, 2, 2, EPI, 2>(g); return true;
-    case 11: launch_ms<256, 256, 32, 4, 2, 4, EPI, 2>(g); return true;
-    case 12: launch_ms<192, 256, 64, 2, 2, 4, EPI, 2>(g); return true;
-    case 13: launch_ms<256, 256, 64, 2, 2, 2, EPI, 2>(g); return true;
-    case 14: launch_ms<256, 128, 32, 3, 2, 2, EPI, 1, 2>(g); return true;   // 2 blocks / CU
-    case 15: launch_ms<128, 256, 32, 3, 2, 2, EPI, 1, 2>(g); return true;
-    case 16: launch_ms<256, 128, 32, 3, 2, 2, EPI, 2, 2>(g); return true;
-    case 17: launch_ms<192, 128, 32, 3, 2, 2, EPI, 1, 2>(g); return true;
-    case 18: launch_ms<128, 128, 64, 2, 2, 2, EPI, 1, 2>(g); return true;
-    case 19: launch_pp<256, EPI>(g); return true;                           // ping-pong
-    case 20: launch_pp<192, EPI>(g); return true;
-    case 21: launch_ms<256, 256, 64, 2, 2, 4, EPI, 1, 1, 1>(g); return true;  // register loader
-    case 22: launch_ms<256, 256, 64, 2, 2, 4, EPI, 0, 1, 1>(g); return true;
-    case 23: launch_ms<192, 256, 64, 2, 2, 4, EPI, 1, 1, 1>(g); return true;
-    case 24: launch_ms<256, 256, 64, 2, 2, 2, EPI, 1, 1, 1>(g); return true;
-    case 25: launch_ms<256, 256, 64, 2, 2, 2, EPI, 1>(g); return true;       // 4 waves 128x128
-    case 26: launch_ms<256, 256, 64, 2, 2, 2, EPI, 3>(g); return true;       // 4 waves, continuous ring
-    case 27: launch_ms<256, 256, 32, 4, 2, 2, EPI, 3>(g); return true;
-    case 28: launch_ms<256, 256, 64, 2, 2, 4, EPI, 3>(g); return true;       // 8 waves, continuous ring
-    case 29: launch_ms<192, 256, 64, 2, 2, 4, EPI, 3>(g); return true;
-    case 30: launch_ms<256, 256, 64, 2, 2, 4, EPI, 1, 1, 2>(g); return true;  // diag: cached loads
-    case 31: launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 2>(g); return true;
-    case 32: launch_ms<192, 256, 64, 2, 2, 2, EPI, 3>(g); return true;
-    case 33: launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 0, 16>(g); return true;  // 16x16x32
-    case 34: launch_ms<192, 256, 64, 2, 2, 2, EPI, 3, 1, 0, 16>(g); return true;
-    case 35: launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 2, 16>(g); return true;  // diag
-    case 36: launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 3>(g); return true;  // diag: no loads
-    case 37: launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 4>(g); return true;  // diag: no frag reads
-    case 38: launch_ms<256, 256, 64, 2, 2, 2, EPI, 3, 1, 5>(g); return true;  // buffer loads
-    case 39: launch_ms<192, 256, 64, 2, 2, 2, EPI, 3, 1, 5>(g); return true;
-    case 40: launch_ms<256, 256, 64, 2, 2, 4, EPI, 1, 1, 5>(g); return true;
-    case 41: launch_ms<192, 256, 64, 2, 2, 4, EPI, 1, 1, 5>(g); return true;
-    case 42: launch_ms<256, 256, 32, 4, 2, 2, EPI, 3, 1, 5>(g); return true;
-    case 43: launch_ms<192, 256, 32, 4, 2, 2, EPI, 3, 1, 5>(g); return true;
-    case 44: launch_ms<256, 256, 32, 3, 2, 2, EPI, 3, 1, 5>(g); return true;
-    case 50: launch_ms<256, 256, 64, 2, 2, 4, EPI, 3, 1, 5>(g); return true;  // 8-wave ring, buffer loads
-    case 51: launch_ms<192, 256, 64, 2, 2, 4, EPI, 3, 1, 5>(g); return true;
-    case 55: launch_ms<256, 256, 64, 2, 2, 4, EPI, 3, 1, 6>(g); return true;  // diag: no epilogue
-    case 56: launch_ms<256, 256, 64, 2, 2, 4, EPI, 4, 1, 5>(g); return true;  // split rings (A 3, B 2)
-    case 57: launch_ms<256, 256, 64, 2, 2, 4, EPI, 5, 1, 5>(g); return true;  // split rings (A 2, B 3)
-    case 68: launch_ms<256, 256, 64, 2, 2, 4, EPI, 4, 1, 5, 16>(g); return true;  // split rings, 16x16x32
-    case 69: launch_ms<256, 256, 64, 2, 2, 4, EPI, 8, 1, 5, 16>(g); return true;  // the same, spread 2
-    case 70: launch_ms<256, 256, 64, 2, 2, 4, EPI, 9, 1, 5, 16>(g); return true;  // reads 2, loads 4
-    case 71: launch_ms<256, 256, 64, 2, 2, 4, EPI, 10, 1, 5, 16>(g); return true; // reads 1, loads 4
-    case 72: launch_ms<256, 256, 64, 2, 4, 2, EPI, 8, 1, 5, 16>(g); return true;  // 4 x 2 waves
-    case 73: launch_ms<256, 256, 64, 2, 2, 4, EPI, 11, 1, 5, 16>(g); return true; // B ring deep
-    case 74: launch_ms<128, 128, 64, 2, 2, 2, EPI, 8, 2, 5, 16>(g); return true;  // small grids, 16x16x32
-    case 75: launch_ms<128, 128, 64, 2, 2, 2, EPI, 4, 2, 5, 16>(g); return true;  // the same, no spread
-    case 76: launch_ms<128, 128, 64, 2, 2, 2, EPI, 3, 2, 5, 16>(g); return true;  // equal-depth rings
-    case 7: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 1>(g); return true;    // diag: compute only
-    case 8: launch_cfg<256, 256, 2, 4, EPI, 0, 8, 1, 2>(g); return true;    // diag: loads only
-    default: return false;
     }
 }
 
 // Tile configuration per shape. The 8-wave 256-wide kernels are the main
 // path; a 192-row tile is taken when it quantises the grid onto the 256 CUs
-// better (M = 8704: 34 -> 46 row tiles), and 128x128 tiles for grids too
-// small to fill the chip twice with 256x256 tiles.
-static int g_family = 0;   // hd_gemm_set_family
-
-extern "C" int hd_gemm_set_family(int family) {
-    const int prev = g_family;
-    g_family = family >= 1 && family <= 3 ? family : 0;
-    return prev;
-}
-
+// better (M = 8704 without a workspace: 34 -> 46 row tiles), and 128x128
+// tiles for grids too small to fill the chip with 256x256 tiles.
 static double quant_eff(long tiles) {
     long rounds = (tiles + 255) / 256;
     return (double)tiles / (double)(rounds * 256);
@@ -1609,81 +907,50 @@ static const char *pick_and_launch(GemmArgs &g, bool launch, void *ws = nullptr,
     const double c256 = tile_cost(t256, 1, 256, 256, g.K, 1.0, p256);
     const double c192 = tile_cost(t192, 1, 192, 256, g.K, 0.9, p192);
     const double c128 = tile_cost(t128, 2, 128, 128, g.K, 0.8, p128);
+    // buffer loads address with 32-bit byte offsets: both operands under 2 GiB
     const bool fits = (size_t)(g.M + 256) * g.K * 2 < ((size_t)1 << 31) &&
                       (size_t)g.N * g.K * 2 < ((size_t)1 << 31);
+    const bool use192 = c192 < c256;
+    const bool split256 = p256 > 1;
+    if (!fits) {
+        // operands of 2 GiB or more: equal-depth rings filled by
+        // global_load_lds (64-bit addresses), the same MFMA tiles and K order
+        if (use192) {
+            if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 3, 1, 0, 16>(g, ws, ws_bytes);
+            return "bf16_192x256x64_w2x4_m16_ring";
+        }
+        if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 3, 1, 0, 16>(g, ws, ws_bytes);
+        return split256 ? "bf16_256x256x64_w2x4_m16_ring_tailsplit" : "bf16_256x256x64_w2x4_m16_ring";
+    }
     // Small grids (the 256 x 256 tiles fill at most one round, K <= 4096, no
-    // SwiGLU): 128 x 128 tiles, two blocks per CU, on 16x16x32 MFMA tiles
-    // with buffer loads and no K split. The vision tower's M = 1728 GEMMs
-    // (K = 1152): 11.5-20 us against 22-27 us on the previous choice (128 x
-    // 128 tiles on 32x32x16 MFMA with a 4-chunk K split); a 1152-token
-    // block's o_proj: equal at block level (507 us per block either way).
+    // SwiGLU): 128 x 128 tiles, two blocks per CU, no K split. The vision
+    // tower's M = 1728 GEMMs (K = 1152): 11.5-20 us against 22-27 us with a
+    // 4-chunk K split; a 1152-token block's o_proj: equal at block level.
     // Longer K (the 12288-deep down projection) and the SwiGLU epilogue stay
     // on the 256-row tiles (120 vs 139-150 us; 192-212 vs 208-223 us).
     const int slots1 = gemm_slots() > 0 ? gemm_slots() : 256;
-    if (g_family != 1 && g_family != 3 && fits && EPI != EPI_SWIGLU && t256 <= slots1 && g.K <= 4096) {
+    if (EPI != EPI_SWIGLU && t256 <= slots1 && g.K <= 4096) {
         if (launch) launch_ms<128, 128, 64, 2, 2, 2, EPI, 8, 2, 5, 16>(g);
         return "bf16_128x128x64_w2x2_occ2_m16";
     }
     if (c128 < c256 && c128 < c192) {
-        if (g_family != 1 && fits) {
-            if (launch) launch_ms<128, 128, 64, 2, 2, 2, EPI, 8, 2, 5, 16>(g, ws, ws_bytes);
-            return p128 > 1 ? "bf16_128x128x64_w2x2_occ2_m16_split" : "bf16_128x128x64_w2x2_occ2_m16";
-        }
-        if (launch) launch_ms<128, 128, 64, 2, 2, 2, EPI, 1, 2>(g, ws, ws_bytes);
-        return p128 > 1 ? "bf16_128x128x64_w2x2_occ2_split" : "bf16_128x128x64_w2x2_occ2";
+        if (launch) launch_ms<128, 128, 64, 2, 2, 2, EPI, 8, 2, 5, 16>(g, ws, ws_bytes);
+        return p128 > 1 ? "bf16_128x128x64_w2x2_occ2_m16_split" : "bf16_128x128x64_w2x2_occ2_m16";
     }
-    // Family 0 (production): 8 waves (2 x 4) of 128x64 on v_mfma_f32_16x16x32_bf16
-    // (8 x 4 accumulator tiles per wave) with one fragment ring across the K
-    // loop and buffer loads straight to LDS (each operand under 2 GiB: 32-bit
-    // byte offsets), the A operand's LDS ring one stage deeper than B's, and
-    // the next k-step's fragment reads and the refill loads placed between
-    // every other MFMA (schedule 8); two waves per SIMD cover each other's
-    // barrier and load-issue stalls. On N(0,1) data the matrix cores sustain
-    // ~14 % more FLOP/s with 16x16x32 than with 32x32x16 instructions under
-    // the power limit. Family 2: the same MFMA tiles with equal-depth operand
-    // rings (schedule 3; the same K order, bit-identical). Family 1: the
-    // previous production kernels on v_mfma_f32_32x32x16_bf16 (kept for
-    // same-process comparisons).
-    const bool use192 = c192 < c256;
-    const bool split256 = p256 > 1;
-    if (g_family == 2 && fits) {
-        if (use192) {
-            if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 3, 1, 5, 16>(g, ws, ws_bytes);
-            return "bf16_192x256x64_w2x4_m16_ring_buf_s3";
-        }
-        if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 3, 1, 5, 16>(g, ws, ws_bytes);
-        return "bf16_256x256x64_w2x4_m16_ring_buf_s3";
-    }
-    if (g_family == 1) {
-        if (use192) {
-            if (fits) {
-                if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 4, 1, 5>(g, ws, ws_bytes);
-                return "bf16_192x256x64_w2x4_ring_buf";
-            }
-            if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 3>(g, ws, ws_bytes);
-            return "bf16_192x256x64_w2x4_ring";
-        }
-        if (fits) {
-            if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 4, 1, 5>(g, ws, ws_bytes);
-            return split256 ? "bf16_256x256x64_w2x4_ring_buf_tailsplit" : "bf16_256x256x64_w2x4_ring_buf";
-        }
-        if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 3>(g, ws, ws_bytes);
-        return split256 ? "bf16_256x256x64_w2x4_ring_tailsplit" : "bf16_256x256x64_w2x4_ring";
-    }
+    // 8 waves (2 x 4) of 128x64 (96x64) on v_mfma_f32_16x16x32_bf16 (8 x 4
+    // accumulator tiles per wave) with one fragment ring across the K loop
+    // and buffer loads straight to LDS, the A operand's LDS ring one stage
+    // deeper than B's, and the next k-step's fragment reads and the refill
+    // loads placed between every other MFMA; two waves per SIMD cover each
+    // other's barrier and load-issue stalls. On N(0,1) data the matrix cores
+    // sustain ~14 % more FLOP/s with 16x16x32 than with 32x32x16
+    // instructions under the power limit.
     if (use192) {
-        if (fits) {
-            if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 8, 1, 5, 16>(g, ws, ws_bytes);
-            return "bf16_192x256x64_w2x4_m16_ring_buf";
-        }
-        if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 3, 1, 0, 16>(g, ws, ws_bytes);
-        return "bf16_192x256x64_w2x4_m16_ring";
+        if (launch) launch_ms<192, 256, 64, 2, 2, 4, EPI, 8, 1, 5, 16>(g, ws, ws_bytes);
+        return "bf16_192x256x64_w2x4_m16_ring_buf";
     }
-    if (fits) {
-        if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 8, 1, 5, 16>(g, ws, ws_bytes);
-        return split256 ? "bf16_256x256x64_w2x4_m16_ring_buf_tailsplit" : "bf16_256x256x64_w2x4_m16_ring_buf";
-    }
-    if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 3, 1, 0, 16>(g, ws, ws_bytes);
-    return split256 ? "bf16_256x256x64_w2x4_m16_ring_tailsplit" : "bf16_256x256x64_w2x4_m16_ring";
+    if (launch) launch_ms<256, 256, 64, 2, 2, 4, EPI, 8, 1, 5, 16>(g, ws, ws_bytes);
+    return split256 ? "bf16_256x256x64_w2x4_m16_ring_buf_tailsplit" : "bf16_256x256x64_w2x4_m16_ring_buf";
 }
 
 static bool mfma_ok(const void *x, const void *y, int N, int K) {
@@ -1739,19 +1006,9 @@ extern "C" int hd_linear_qkv_rope_ws(const void *x, const void *wq, const void *
     const bool split256 =
         ws && tail_split_of(t256, hidden / 64, (size_t)256 * 256 * 4, ws_bytes, (size_t)256 * 256 * 2) > 1;
     const bool use192 = !split256 && quant_eff(t192) > quant_eff(t256) * 1.12;
-    if (g_family != 1) {   // 8 waves: two 64-wide wave tiles per head, 16x16x32 MFMA tiles
-        if (g_family == 2) {
-            if (use192) launch_ms<192, 256, 64, 2, 2, 4, EPI_QKV, 3, 1, 5, 16>(g, ws, ws ? ws_bytes : 0);
-            else launch_ms<256, 256, 64, 2, 2, 4, EPI_QKV, 3, 1, 5, 16>(g, ws, ws ? ws_bytes : 0);
-        } else if (use192) {
-            launch_ms<192, 256, 64, 2, 2, 4, EPI_QKV, 8, 1, 5, 16>(g, ws, ws ? ws_bytes : 0);
-        } else {
-            launch_ms<256, 256, 64, 2, 2, 4, EPI_QKV, 8, 1, 5, 16>(g, ws, ws ? ws_bytes : 0);
-        }
-    } else {
-        if (use192) launch_ms<192, 256, 64, 2, 2, 2, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
-        else launch_ms<256, 256, 64, 2, 2, 2, EPI_QKV, 3, 1, 5>(g, ws, ws ? ws_bytes : 0);
-    }
+    // 8 waves: two 64-wide wave tiles per head, 16x16x32 MFMA tiles
+    if (use192) launch_ms<192, 256, 64, 2, 2, 4, EPI_QKV, 8, 1, 5, 16>(g, ws, ws ? ws_bytes : 0);
+    else launch_ms<256, 256, 64, 2, 2, 4, EPI_QKV, 8, 1, 5, 16>(g, ws, ws ? ws_bytes : 0);
     hd_check_launch("linear_qkv_rope");
     return 0;
 }
@@ -1762,23 +1019,6 @@ extern "C" int hd_linear_qkv_rope(const void *x, const void *wq, const void *wk,
                                   int hidden, float eps) {
     return hd_linear_qkv_rope_ws(x, wq, wk, wv, qn_w, kn_w, cs, q, k, vt, batch, seq, heads,
                                  kv_heads, hidden, eps, nullptr, 0);
-}
-
-// Diagnostics: runs tuning-table configuration `cfg` (0..35) for
-// epilogue 0 (plain) or 3 (SwiGLU, w1 = up). Returns 0 when launched.
-extern "C" int hd_gemm_tune_run(int cfg, int epi, const void *x, const void *w0, const void *w1,
-                                void *y, int M, int N, int K) {
-    if (!x || !w0 || !y || M <= 0 || N <= 0 || K <= 0 || !mfma_ok(x, y, N, K)) return 1;
-    GemmArgs g = {};
-    g.A = (const uint16_t *)x;
-    g.B[0] = g.B[2] = (const uint16_t *)w0;
-    g.B[1] = (const uint16_t *)(w1 ? w1 : w0);
-    g.seg_end[0] = g.seg_end[1] = g.seg_end[2] = N;
-    g.C = (uint16_t *)y;
-    g.M = M; g.N = N; g.K = K; g.ldc = N;
-    bool ok = epi == EPI_SWIGLU ? (w1 && run_table<EPI_SWIGLU>(cfg, g)) : run_table<EPI_NONE>(cfg, g);
-    if (!ok) return 1;
-    return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
 // Matrix-core ceiling probe (diagnostic): every wave runs 8 independent

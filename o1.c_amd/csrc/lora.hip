@@ -1,13 +1,11 @@
 // GPU LoRA merge-on-load: W = bf16(float(W) + s * (up @ down)), fp32 delta.
 // Replaces hd_lora_merge_gpu (lora_merge.cu:35-104). One launch per target;
-// the delta never reaches HBM and nothing is allocated. Three kernels:
-//  - lora_merge_stream_kernel (default for R <= 64): persistent blocks
+// the delta never reaches HBM and nothing is allocated. Two kernels:
+//  - lora_merge_stream_kernel (R <= 64, R % 4 == 0): persistent blocks
 //    stream W through an LDS ring, rank product on the bf16 matrix cores
 //    with fp32 operands split in three bf16 parts;
-//  - lora_merge_mfma_kernel (any R): a block per 128 x 128 tile, rank
-//    product on the fp32 matrix cores (v_mfma_f32_32x32x2_f32);
-//  - lora_merge_split_kernel: the tile-per-block form of the split rank
-//    product (comparisons).
+//  - lora_merge_mfma_kernel (any other R): a block per 128 x 128 tile, rank
+//    product on the fp32 matrix cores (v_mfma_f32_32x32x2_f32).
 #include <stdio.h>
 
 #include "hd_common.hpp"
@@ -26,7 +24,7 @@
 #define LM_SD (LM_RC * (LM_T + 32))         // down slice [r][col], +32: the half-waves read
                                             // consecutive r rows in opposite bank halves
 #define LM_ST (LM_T * (LM_T + 8))           // fp32 delta tile [row][col] for the W update
-template <int OCC, bool UNROLL = true>
+template <int OCC>
 __global__ __launch_bounds__(256, OCC) void lora_merge_mfma_kernel(uint16_t *__restrict__ w,
                                                               const float *__restrict__ up,
                                                               const float *__restrict__ down, int N,
@@ -90,7 +88,7 @@ __global__ __launch_bounds__(256, OCC) void lora_merge_mfma_kernel(uint16_t *__r
                 acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[j], 0, 0, 0);
             }
         };
-        if (UNROLL && rc == LM_RC) {
+        if (rc == LM_RC) {
             // unrolled: the operand reads of later steps issue ahead of the
             // MFMAs instead of one LDS round trip per step
 #pragma unroll
@@ -145,148 +143,12 @@ __global__ __launch_bounds__(256, OCC) void lora_merge_mfma_kernel(uint16_t *__r
 // v_mfma_f32_32x32x16_bf16 per 16 ranks replace eight v_mfma_f32_32x32x2_f32,
 // about 2.7x less matrix-core time: the merge becomes bound by the
 // read-modify-write of W in HBM. Ranks are staged 32 at a time: the six part
-// planes of the up slice [row][r] and of the transposed down slice [col][r]
-// (61 KB) share the LDS with the fp32 delta tile, two blocks per CU.
-#define LS_RC 32
-#define LS_LD (LS_RC + 8)                   // plane row stride (bf16): conflict-free 16-byte reads
-#define LS_PL (LM_T * LS_LD)                // one part plane
+// planes of the up slice and of the transposed down slice are staged in LDS.
 __device__ __forceinline__ void split3(float x, uint16_t &h0, uint16_t &h1, uint16_t &h2) {
     h0 = f2bf(x);
     const float r1 = x - bf2f(h0);
     h1 = f2bf(r1);
     h2 = f2bf(r1 - bf2f(h1));
-}
-template <int OCC>
-__global__ __launch_bounds__(256, OCC) void lora_merge_split_kernel(uint16_t *__restrict__ w,
-                                                                 const float *__restrict__ up,
-                                                                 const float *__restrict__ down, int N,
-                                                                 int K, int R, float scale) {
-    constexpr int PLANES = 6 * LS_PL * 2, STB = LM_ST * 4;
-    __shared__ __attribute__((aligned(16))) unsigned char lds_raw[PLANES > STB ? PLANES : STB];
-    uint16_t *const pu = (uint16_t *)lds_raw;        // up planes 0..2
-    uint16_t *const pd = pu + 3 * LS_PL;             // down^T planes 0..2
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int n0 = blockIdx.y * LM_T, k0 = blockIdx.x * LM_T;
-    const int l32 = lane & 31, lh = lane >> 5;
-    const bool full = n0 + LM_T <= N && k0 + LM_T <= K && K % 8 == 0;
-    u32x4_t wch[8];
-    f32x16_t acc[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) acc[j][e] = 0.f;
-    // staging roles: up - row ur, ranks ur4 .. ur4+3 (four rows per thread);
-    // down - columns dc4 .. dc4+3, ranks dr4 .. dr4+3
-    const int ur = threadIdx.x / 8, ur4 = (threadIdx.x % 8) * 4;
-    const int dc4 = (threadIdx.x % 32) * 4, dr4 = (threadIdx.x / 32) * 4;
-    for (int r0 = 0; r0 < R; r0 += LS_RC) {
-        float uv[4][4], dv[4][4];   // up: [row block][r]; down: [r][col]
-        const bool fast = full && r0 + LS_RC <= R && R % 4 == 0;
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int row = ur + t * 32;
-            if (fast) {
-                const float4 u = *(const float4 *)(up + (size_t)(n0 + row) * R + r0 + ur4);
-                uv[t][0] = u.x; uv[t][1] = u.y; uv[t][2] = u.z; uv[t][3] = u.w;
-                const float4 d = *(const float4 *)(down + (size_t)(r0 + dr4 + t) * K + k0 + dc4);
-                dv[t][0] = d.x; dv[t][1] = d.y; dv[t][2] = d.z; dv[t][3] = d.w;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int r = r0 + ur4 + e, n = n0 + row;
-                    uv[t][e] = r < R && n < N ? up[(size_t)n * R + r] : 0.f;
-                    const int rd = r0 + dr4 + t, k = k0 + dc4 + e;
-                    dv[t][e] = rd < R && k < K ? down[(size_t)rd * K + k] : 0.f;
-                }
-            }
-        }
-        if (r0 > 0) __syncthreads();   // the previous chunk's planes are read
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            uint16_t h[3][4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) split3(uv[t][e], h[0][e], h[1][e], h[2][e]);
-#pragma unroll
-            for (int p = 0; p < 3; p++) {
-                u32x2_t v = {(uint32_t)h[p][0] | ((uint32_t)h[p][1] << 16),
-                             (uint32_t)h[p][2] | ((uint32_t)h[p][3] << 16)};
-                *(u32x2_t *)(pu + p * LS_PL + (ur + t * 32) * LS_LD + ur4) = v;
-            }
-        }
-#pragma unroll
-        for (int e = 0; e < 4; e++) {   // column dc4 + e: ranks dr4 .. dr4+3
-            uint16_t h[3][4];
-#pragma unroll
-            for (int t = 0; t < 4; t++) split3(dv[t][e], h[0][t], h[1][t], h[2][t]);
-#pragma unroll
-            for (int p = 0; p < 3; p++) {
-                u32x2_t v = {(uint32_t)h[p][0] | ((uint32_t)h[p][1] << 16),
-                             (uint32_t)h[p][2] | ((uint32_t)h[p][3] << 16)};
-                *(u32x2_t *)(pd + p * LS_PL + (dc4 + e) * LS_LD + dr4) = v;
-            }
-        }
-        __syncthreads();
-        if (r0 == 0 && full) {
-            // W chunks of this thread (8 x 8 weights): issued after the first
-            // rank slice is staged, so that staging does not wait behind
-            // them and their latency hides under the MFMAs
-#pragma unroll
-            for (int t = 0; t < 8; t++) {
-                const int c = threadIdx.x + t * 256, row = c / 16, col = (c % 16) * 8;
-                wch[t] = *(const u32x4_t *)(w + (size_t)(n0 + row) * K + k0 + col);
-            }
-        }
-#pragma unroll
-        for (int ks = 0; ks < LS_RC / 16; ks++) {
-            const int rr = ks * 16 + lh * 8;
-            bf16x8_t a[3];
-#pragma unroll
-            for (int p = 0; p < 3; p++) a[p] = *(const bf16x8_t *)(pu + p * LS_PL + (wave * 32 + l32) * LS_LD + rr);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                bf16x8_t b[3];
-#pragma unroll
-                for (int p = 0; p < 3; p++) b[p] = *(const bf16x8_t *)(pd + p * LS_PL + (j * 32 + l32) * LS_LD + rr);
-                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc[j], 0, 0, 0);
-                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc[j], 0, 0, 0);
-                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], acc[j], 0, 0, 0);
-                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], acc[j], 0, 0, 0);
-                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], acc[j], 0, 0, 0);
-                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc[j], 0, 0, 0);
-            }
-        }
-    }
-    __syncthreads();   // planes read: the delta tile reuses the LDS
-    float *st = (float *)lds_raw;
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-#pragma unroll
-        for (int e = 0; e < 16; e++)
-            st[(wave * 32 + (e >> 2) * 8 + lh * 4 + (e & 3)) * (LM_T + 8) + j * 32 + l32] = acc[j][e];
-    __syncthreads();
-    if (full) {
-#pragma unroll
-        for (int t = 0; t < 8; t++) {
-            const int c = threadIdx.x + t * 256, row = c / 16, col = (c % 16) * 8;
-            const float4 d0 = *(const float4 *)(st + row * (LM_T + 8) + col);
-            const float4 d1 = *(const float4 *)(st + row * (LM_T + 8) + col + 4);
-            const float dd[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-            u32x4_t o;
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                o[e] = pack_bf2(fmaf(scale, dd[2 * e], lo_bf(wch[t][e])),
-                                fmaf(scale, dd[2 * e + 1], hi_bf(wch[t][e])));
-            *(u32x4_t *)(w + (size_t)(n0 + row) * K + k0 + col) = o;
-        }
-    } else {
-        for (int c = threadIdx.x; c < LM_T * LM_T; c += 256) {
-            const int row = c / LM_T, col = c % LM_T, n = n0 + row, k = k0 + col;
-            if (n < N && k < K) {
-                const size_t o = (size_t)n * K + k;
-                w[o] = f2bf(fmaf(scale, st[row * (LM_T + 8) + col], bf2f(w[o])));
-            }
-        }
-    }
 }
 
 // Streaming merge for R <= 64 (R % 4 == 0, K % 8 == 0): a persistent block of
@@ -296,8 +158,8 @@ __global__ __launch_bounds__(256, OCC) void lora_merge_split_kernel(uint16_t *__
 //    ahead, into a ring of three 16 KB slots; the update reads W from LDS in
 //    the accumulator layout, writes the bf16 result back in place, and the
 //    tile leaves with coalesced 16-byte buffer stores;
-//  - the rank product uses the part products of lora_merge_split_kernel
-//    (six bf16 part products per fp32 product, here in three accumulators); the up strip's part planes
+//  - the rank product uses the three-part split above (six bf16 part
+//    products per fp32 product, in three accumulators); the up strip's part planes
 //    are staged once per row strip, the down slice's once per tile, into one
 //    of two plane buffers, from registers loaded a tile ahead, while the
 //    previous tile's MFMAs run (two barriers per tile);
@@ -539,18 +401,6 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
 #endif
 }
 
-// hd_lora_set_family: 0 = the streaming split-operand kernel where it
-// applies (R <= 64, R % 4 == 0, K % 8 == 0, W under 2 GiB), else the fp32
-// matrix-core kernel (default); 1 = always the fp32 matrix-core kernel with
-// the unrolled rank loop; 2 = the same with the rolled loop; 3 = the
-// one-tile-per-block split-operand kernel (same-process comparisons)
-static int g_lora_family = 0;
-extern "C" int hd_lora_set_family(int family) {
-    const int prev = g_lora_family;
-    g_lora_family = family >= 1 && family <= 3 ? family : 0;
-    return prev;
-}
-
 extern "C" hd_status hd_lora_merge_gpu(hd_lora_entry *entries, size_t count, void *stream) {
     if (count == 0) return HD_OK;
     if (!entries) {
@@ -573,7 +423,10 @@ extern "C" hd_status hd_lora_merge_gpu(hd_lora_entry *entries, size_t count, voi
         const float scale = e->multiplier * e->alpha / (float)e->rank;   // lora_merge.cu:54
         dim3 grid(hd_cdiv(K, LM_T), hd_cdiv(N, LM_T));
         const bool stream_ok = R <= 64 && R % 4 == 0 && K % 8 == 0 && (size_t)N * K * 2 < ((size_t)1 << 31);
-        if (g_lora_family == 0 && stream_ok) {
+        // the streaming split-operand kernel where it applies (R <= 64,
+        // R % 4 == 0, K % 8 == 0, W under 2 GiB), else the fp32 matrix-core
+        // kernel
+        if (stream_ok) {
             const int ntk = hd_cdiv(K, LT_K), total = hd_cdiv(N, LT_N) * ntk;
             int cus = 0, dev = 0;
             if (hipGetDevice(&dev) != hipSuccess ||
@@ -582,12 +435,6 @@ extern "C" hd_status hd_lora_merge_gpu(hd_lora_entry *entries, size_t count, voi
             lora_merge_stream_kernel<<<total < cus ? total : cus, 512, 0, st>>>(
                 (uint16_t *)e->base_dev, (const float *)e->up_dev, (const float *)e->down_dev, N, K, R, scale,
                 ntk, total);
-        } else if (g_lora_family == 3) {
-            lora_merge_split_kernel<2><<<grid, 256, 0, st>>>((uint16_t *)e->base_dev, (const float *)e->up_dev,
-                                                             (const float *)e->down_dev, N, K, R, scale);
-        } else if (g_lora_family == 2) {
-            lora_merge_mfma_kernel<2, false><<<grid, 256, 0, st>>>((uint16_t *)e->base_dev, (const float *)e->up_dev,
-                                                            (const float *)e->down_dev, N, K, R, scale);
         } else {
             lora_merge_mfma_kernel<2><<<grid, 256, 0, st>>>((uint16_t *)e->base_dev, (const float *)e->up_dev,
                                                             (const float *)e->down_dev, N, K, R, scale);

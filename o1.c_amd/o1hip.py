@@ -236,10 +236,7 @@ SIGNATURES = {
     "hd_linear_swiglu_ws": (None, [P, P, P, P, c_int, c_int, c_int, P, ctypes.c_int64]),
     "hd_linear_concat3": (None, [P, P, c_int, P, c_int, P, c_int, P, c_int, c_int]),
     "hd_gemm_config_name": (c_char_p, [c_int, c_int, c_int, c_int]),
-    "hd_gemm_tune_run": (c_int, [c_int, c_int, P, P, P, P, c_int, c_int, c_int]),
     "hd_mfma_probe": (ctypes.c_double, [P, c_int, c_int, c_int, c_int, P]),
-    "hd_gemm_set_family": (c_int, [c_int]),
-    "hd_flash_set_family": (c_int, [c_int]),
     "hd_tokenizer_load": (c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p]),
     "hd_tokenizer_unload": (None, []),
     "hd_tokenizer_encode": (c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.POINTER(c_int)), ctypes.POINTER(c_size_t)]),
@@ -303,7 +300,6 @@ SIGNATURES = {
                                    c_int, c_int, c_int, c_int, ctypes.POINTER(hd_forward_diagnostics), P, P]),
     # hd_lora.h
     "hd_lora_merge_gpu": (c_int, [ctypes.POINTER(hd_lora_entry), c_size_t, P]),
-    "hd_lora_set_family": (c_int, [c_int]),
     "hd_lora_apply": (c_int, [ctypes.POINTER(hd_lora_config), ctypes.POINTER(hd_weight_store), c_int]),
     "hd_lora_last_error": (c_char_p, []),
     # hd_host.h
