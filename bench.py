@@ -441,7 +441,7 @@ def time_c0(pkg, lib, block, b0, dev, steps, warmup, kernel_iters):
             "gemm": {"kernel": "gemm_bf16 gate/up + SwiGLU epilogue", "bound": "mfma",
                      "achieved": round(kflop / (kms * 1e-3) / 1e12, 1), "peak": PEAK_BF16 / 1e12,
                      "unit": "TFLOP/s", "frac": round(kflop / (kms * 1e-3) / PEAK_BF16, 4),
-                     "traffic": None, "launch_ms": round(kms, 4), "shape": [S, 2 * FF, HID]}}
+                     "traffic": read_traffic("c0"), "launch_ms": round(kms, 4), "shape": [S, 2 * FF, HID]}}
 
 
 def run_c0(pkg, lib, cfg, args, dev):

@@ -95,6 +95,55 @@ def test_forward_vs_oracle(pkg, lib, dev, split):
         assert r <= bound and c >= 0.9999 and rb <= bound
 
 
+def test_forward_device_section_matches_config(pkg, lib, dev):
+    """hd_forward's sec_dev (the MRoPE section in device memory, as the
+    reference passes secd to every forward, generate.c:1341) gives the
+    forward the same values as that section set through the block config,
+    bit for bit; a non-default section ([32, 16, 16] against the default [24,
+    20, 20]) changes the output, so the argument is not ignored."""
+    nL, HID, H, KV, FF, D = 2, 512, 4, 2, 1024, 128
+    T, gh, gw = 24, 8, 10
+    I = gh * gw
+    S = T + I
+    fw = make_forward_weights(nL, HID, H, KV, FF, D, seed=12)
+    rng = np.random.default_rng(4)
+    ids = rng.integers(0, 151643, T).astype(np.int64)
+    ids[-1] = TMS
+    vin = bf16(torch.from_numpy(rng.standard_normal((I, 3072)).astype(np.float32))).numpy()
+    pos = grid_pos(T, gh, gw)
+    tens = {k: v.to(dev, torch.bfloat16) for k, v in store_names(fw).items()}
+    ws_store = pkg.WeightStore(tens)
+    fb = pkg.hd_forward_binding()
+    pkg.check_status(lib.hd_forward_resolve(ctypes.byref(ws_store.store), nL, ctypes.byref(fb)), "resolve")
+    wsbuf = torch.empty(lib.hd_forward_workspace_bytes(S, I, H, KV, HID, FF, D, None), dtype=torch.uint8,
+                        device=dev)
+    ws = pkg.hd_forward_workspace()
+    ws.hidden_a = wsbuf.data_ptr()
+    idsd, posd = torch.from_numpy(ids).to(dev), torch.from_numpy(pos).to(dev)
+    vind = torch.from_numpy(vin).to(dev, torch.bfloat16)
+    td = torch.tensor([0.61], dtype=torch.float32, device=dev)
+    sec = (32, 16, 16)
+    secd = torch.tensor(sec, dtype=torch.int64, device=dev)
+
+    def run(sec_ptr):
+        out = torch.empty(S, 3072, dtype=torch.bfloat16, device=dev)
+        st = lib.hd_forward(ctypes.byref(fb), ctypes.byref(ws), pkg.ptr(idsd), T, pkg.ptr(posd), None,
+                            pkg.ptr(vind), I, None, pkg.ptr(td), sec_ptr, S, H, KV, HID, FF, D, TMS, None,
+                            pkg.ptr(out), None)
+        pkg.check_status(st, "hd_forward")
+        torch.cuda.synchronize()
+        return out
+
+    pkg.set_block_config(theta=1e4)                   # default section [24, 20, 20]
+    dflt = run(None)
+    via_dev = run(pkg.ptr(secd))
+    pkg.set_block_config(theta=1e4, section=sec)
+    via_cfg = run(None)
+    lib.hd_forward_binding_free(ctypes.byref(fb))
+    assert torch.equal(via_dev, via_cfg)
+    assert not torch.equal(via_dev, dflt)
+
+
 def test_forward_batched_matches_single(pkg, lib, dev):
     import importlib
     synth = importlib.import_module("o1c_amd.synthetic")
