@@ -76,7 +76,13 @@ const char *hd_lora_last_error(void);
 
 /* include/hd_lora.h:75. `stream` is a hipStream_t (NULL = library stream).
  * Returns HD_OK, HD_ERR_MISSING on a null pointer, HD_ERR_UNSUPPORTED on a
- * rank above 256, HD_ERR_RUNTIME on a launch failure. */
+ * rank above 256, HD_ERR_RUNTIME on a launch failure (every entry is
+ * checked before the GPU is touched). Entries of one (out, in, rank) shape
+ * that the streaming kernel takes merge in one launch; entries on the same
+ * weight merge in entry order. Like the reference's merge (which allocates
+ * and frees a delta scratch per call), the call allocates a small device
+ * list of the batched targets (32 bytes each), and synchronises `stream`
+ * before freeing it. */
 hd_status hd_lora_merge_gpu(hd_lora_entry *entries, size_t count, void *stream);
 
 

@@ -1,12 +1,15 @@
 // GPU LoRA merge-on-load: W = bf16(float(W) + s * (up @ down)), fp32 delta.
 // Replaces hd_lora_merge_gpu (lora_merge.cu:35-104). One launch per target;
-// the delta never reaches HBM and nothing is allocated. Two kernels:
+// the delta never reaches HBM. Two kernels:
 //  - lora_merge_stream_kernel (R <= 64, R % 4 == 0): persistent blocks
 //    stream W through an LDS ring, rank product on the bf16 matrix cores
 //    with fp32 operands split in three bf16 parts;
 //  - lora_merge_mfma_kernel (any other R): a block per 128 x 128 tile, rank
 //    product on the fp32 matrix cores (v_mfma_f32_32x32x2_f32).
 #include <stdio.h>
+
+#include <map>
+#include <vector>
 
 #include "hd_common.hpp"
 #include "../../include/hd_hip.h"
@@ -179,10 +182,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t lt_rsrc(const void *base, uint
     return __builtin_amdgcn_make_buffer_rsrc((void *)(((uint64_t)hi << 32) | lo), 0,
                                              __builtin_amdgcn_readfirstlane(nbytes), 0x00020000);
 }
-__global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__restrict__ w,
-                                                                 const float *__restrict__ up,
-                                                                 const float *__restrict__ down, int N,
-                                                                 int K, int R, float scale, int ntk,
+// One launch merges every target of a batch that shares (N, K, R): the
+// tiles of all of them form one index space (target-major, then row strip,
+// then column tile) that the persistent blocks split evenly, so small
+// targets (the 1024-row k / v projections) no longer pay a launch and a
+// pipeline fill each.
+struct LmTarget {
+    uint16_t *w;
+    const float *up;
+    const float *down;
+    float scale;
+};
+__global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(const LmTarget *__restrict__ tg, int N,
+                                                                 int K, int R, int ntk, int nstrip,
                                                                  int total) {
     __shared__ __attribute__((aligned(1024))) uint16_t wring[3][LT_N * LT_K];
     __shared__ __attribute__((aligned(16))) uint16_t upl[3][LT_N * LT_LD];
@@ -194,8 +206,9 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
     const int te = (int)((int64_t)(blockIdx.x + 1) * total / gridDim.x);
     if (tb >= te) return;
     const uint32_t OOB = 0x80000000u;
-    const __amdgpu_buffer_rsrc_t rw = lt_rsrc(w, (uint32_t)((size_t)N * K * 2));
-    const __amdgpu_buffer_rsrc_t ru = lt_rsrc(up, (uint32_t)((size_t)N * R * 4));
+    const uint32_t w_bytes = (uint32_t)((size_t)N * K * 2), u_bytes = (uint32_t)((size_t)N * R * 4),
+                   d_bytes = (uint32_t)((size_t)R * K * 4);
+    const int tpt = nstrip * ntk;   // tiles per target
     // Each wave owns the 32 x 32 sub-tile of W its accumulator covers (rows
     // nblk*32.., columns kblk*32..) and alone loads, updates and stores it,
     // so W needs no barrier. Its 2 KB in a ring slot: instruction i, lane L
@@ -214,14 +227,29 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
     // incrementally: a division by the runtime ntk costs tens of scalar
     // instructions, and every wave needs them for three tiles per step
     struct TC {
-        int tn, tk;
-        bool ok;   // the tile exists (t < te)
+        int g, tn, tk;   // target, row strip, column tile
+        bool ok;         // the tile exists (t < te)
+        uint16_t *w;     // the target's tensors and scale (wave-uniform)
+        const float *up, *down;
+        float scale;
+    };
+    auto tc_load = [&](TC &c) {
+        const int gg = c.g < total / tpt ? c.g : 0;   // past the last target: any valid entry
+        c.w = tg[gg].w;
+        c.up = tg[gg].up;
+        c.down = tg[gg].down;
+        c.scale = tg[gg].scale;
     };
     auto tc_next = [&](TC c, int t_next) {
         c.tk++;
         if (c.tk == ntk) {
             c.tk = 0;
             c.tn++;
+            if (c.tn == nstrip) {
+                c.tn = 0;
+                c.g++;
+                tc_load(c);
+            }
         }
         c.ok = t_next < te;
         return c;
@@ -232,16 +260,17 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
     };
     auto issue_w = [&](const TC &c, int sl) {
         uint16_t *sub = wring[sl] + wave * 1024;
+        const __amdgpu_buffer_rsrc_t rw = lt_rsrc(c.w, w_bytes);
 #pragma unroll
         for (int i = 0; i < 2; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (HD_LDS void *)(sub + i * 512), 16, w_off(c, i), 0, 0,
                                                      0);
     };
     // down slice of a tile: ranks rr, rr + 1, columns kc .. kc + 3
-    const __amdgpu_buffer_rsrc_t rd = lt_rsrc(down, (uint32_t)((size_t)R * K * 4));
     const int kc = (tid % 16) * 4, rr = (tid / 16) * 2;
     f32x4_t DA[2], DB[2];
     auto load_down = [&](const TC &c, f32x4_t (&d)[2]) {
+        const __amdgpu_buffer_rsrc_t rd = lt_rsrc(c.down, d_bytes);
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int r = rr + j, gk = c.tk * LT_K + kc;
@@ -261,8 +290,9 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
                 *(uint32_t *)(dpl[b][pl] + (kc + e) * LT_LD + rr) = (uint32_t)h0[pl] | ((uint32_t)h1[pl] << 16);
         }
     };
-    auto stage_up = [&](int tn) {   // the up strip's part planes; drains the queue
-        const int row = tid / 4, r16 = (tid % 4) * 16, gn = tn * LT_N + row;
+    auto stage_up = [&](const TC &c) {   // the up strip's part planes; drains the queue
+        const __amdgpu_buffer_rsrc_t ru = lt_rsrc(c.up, u_bytes);
+        const int row = tid / 4, r16 = (tid % 4) * 16, gn = c.tn * LT_N + row;
         float uv[16];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -287,7 +317,12 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
             }
     };
     // prologue: W(tb), down(tb), W(tb+1), down(tb+1); the planes of tile tb
-    TC c0 = {tb / ntk, tb % ntk, true};   // tile t
+    TC c0;                                // tile t
+    c0.g = tb / tpt;
+    c0.tn = (tb % tpt) / ntk;
+    c0.tk = tb % ntk;
+    c0.ok = true;
+    tc_load(c0);
     TC c1 = tc_next(c0, tb + 1);          // tile t + 1
     TC c2 = tc_next(c1, tb + 2);          // tile t + 2
     int sl = 0;                           // ring slot of tile t
@@ -295,8 +330,8 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
     load_down(c0, DA);
     issue_w(c1, 1);
     load_down(c1, DB);
-    int staged_tn = c0.tn;
-    stage_up(staged_tn);   // vmcnt(0): down(tb) landed as well
+    int staged = c0.g * nstrip + c0.tn;   // target and row strip of the staged up planes
+    stage_up(c0);          // vmcnt(0): down(tb) landed as well
     put_down(DA, tb & 1);
     // tile t splits down(t+1) (registers dsplit) for the next tile and loads
     // down(t+2) into the registers down(t) used (dload); the loop runs two
@@ -306,9 +341,9 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
         // the planes of tile t are written; every wave is past the previous
         // tile's MFMAs (the other plane buffer is free)
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (c0.tn != staged_tn) {
-            stage_up(c0.tn);
-            staged_tn = c0.tn;
+        if (c0.g * nstrip + c0.tn != staged) {
+            stage_up(c0);
+            staged = c0.g * nstrip + c0.tn;
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         }
         // the MFMAs of tile t; the next tile's down slice is split into the
@@ -369,10 +404,10 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
             u32x2_t o[4];
 #pragma unroll
             for (int q = 0; q < 4; q++)
-                o[q] = (u32x2_t){pack_bf2(fmaf(scale, acc[4 * q], lo_bf(wv[q][0])),
-                                          fmaf(scale, acc[4 * q + 1], hi_bf(wv[q][0]))),
-                                 pack_bf2(fmaf(scale, acc[4 * q + 2], lo_bf(wv[q][1])),
-                                          fmaf(scale, acc[4 * q + 3], hi_bf(wv[q][1])))};
+                o[q] = (u32x2_t){pack_bf2(fmaf(c0.scale, acc[4 * q], lo_bf(wv[q][0])),
+                                          fmaf(c0.scale, acc[4 * q + 1], hi_bf(wv[q][0]))),
+                                 pack_bf2(fmaf(c0.scale, acc[4 * q + 2], lo_bf(wv[q][1])),
+                                          fmaf(c0.scale, acc[4 * q + 3], hi_bf(wv[q][1])))};
             asm volatile(
                 "ds_write_b64 %0, %1\n\tds_write_b64 %2, %3\n\tds_write_b64 %4, %5\n\tds_write_b64 %6, %7"
                 :
@@ -380,6 +415,7 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(uint16_t *__r
                 : "memory");
         }
         // the sub-tile leaves as it arrived (same lanes, same offsets)
+        const __amdgpu_buffer_rsrc_t rw = lt_rsrc(c0.w, w_bytes);
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             const uint32_t sa = (uint32_t)(size_t)(HD_LDS void *)(sub + (i * 64 + lane) * 8);
@@ -408,6 +444,7 @@ extern "C" hd_status hd_lora_merge_gpu(hd_lora_entry *entries, size_t count, voi
         return HD_ERR_MISSING;
     }
     hipStream_t st = stream ? (hipStream_t)stream : hd_stream();
+    // every entry is checked before the GPU is touched
     for (size_t i = 0; i < count; i++) {
         hd_lora_entry *e = &entries[i];
         if (!e->base_dev || !e->up_dev || !e->down_dev || e->rank == 0 || e->in_dim == 0 ||
@@ -419,31 +456,98 @@ extern "C" hd_status hd_lora_merge_gpu(hd_lora_entry *entries, size_t count, voi
             hd_set_error("lora: entry %zu rank %u > 256", i, e->rank);
             return HD_ERR_UNSUPPORTED;
         }
+    }
+    // Batches. An entry's level is one past the level of the last earlier
+    // entry on the same weight (two adapters on one target merge in entry
+    // order, as the reference's loop does); levels launch in order. Within a
+    // level, the entries the streaming kernel takes (R <= 64, R % 4 == 0,
+    // K % 8 == 0, W under 2 GiB) go into one launch per (N, K, R); the others
+    // run the fp32 matrix-core kernel, one launch each.
+    struct Key {
+        int level, N, K, R;
+        bool operator<(const Key &o) const {
+            return level != o.level ? level < o.level
+                                    : (N != o.N ? N < o.N : (K != o.K ? K < o.K : R < o.R));
+        }
+    };
+    std::map<const void *, int> last;
+    std::map<Key, std::vector<LmTarget>> stream_batches;
+    std::vector<std::pair<int, size_t>> mfma_entries;   // (level, entry)
+    int nlevels = 0;
+    for (size_t i = 0; i < count; i++) {
+        hd_lora_entry *e = &entries[i];
+        auto it = last.find(e->base_dev);
+        const int level = it == last.end() ? 0 : it->second + 1;
+        last[e->base_dev] = level;
+        nlevels = level + 1 > nlevels ? level + 1 : nlevels;
         const int N = (int)e->out_dim, K = (int)e->in_dim, R = (int)e->rank;
         const float scale = e->multiplier * e->alpha / (float)e->rank;   // lora_merge.cu:54
-        dim3 grid(hd_cdiv(K, LM_T), hd_cdiv(N, LM_T));
         const bool stream_ok = R <= 64 && R % 4 == 0 && K % 8 == 0 && (size_t)N * K * 2 < ((size_t)1 << 31);
-        // the streaming split-operand kernel where it applies (R <= 64,
-        // R % 4 == 0, K % 8 == 0, W under 2 GiB), else the fp32 matrix-core
-        // kernel
-        if (stream_ok) {
-            const int ntk = hd_cdiv(K, LT_K), total = hd_cdiv(N, LT_N) * ntk;
-            int cus = 0, dev = 0;
-            if (hipGetDevice(&dev) != hipSuccess ||
-                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-                cus = 256;
-            lora_merge_stream_kernel<<<total < cus ? total : cus, 512, 0, st>>>(
-                (uint16_t *)e->base_dev, (const float *)e->up_dev, (const float *)e->down_dev, N, K, R, scale,
-                ntk, total);
-        } else {
+        if (stream_ok)
+            stream_batches[Key{level, N, K, R}].push_back(
+                LmTarget{(uint16_t *)e->base_dev, (const float *)e->up_dev, (const float *)e->down_dev, scale});
+        else
+            mfma_entries.push_back({level, i});
+    }
+    // the batches' target lists in one small device buffer (freed after the
+    // stream has run the launches, as the reference frees its delta scratch)
+    size_t ntg = 0;
+    for (auto &b : stream_batches) ntg += b.second.size();
+    std::vector<LmTarget> host_tg;
+    host_tg.reserve(ntg);
+    for (auto &b : stream_batches) host_tg.insert(host_tg.end(), b.second.begin(), b.second.end());
+    LmTarget *dev_tg = nullptr;
+    if (ntg) {
+        if (hipMalloc((void **)&dev_tg, ntg * sizeof(LmTarget)) != hipSuccess) {
+            hd_set_error("lora: target list allocation failed");
+            return HD_ERR_OOM;
+        }
+        if (hipMemcpyAsync(dev_tg, host_tg.data(), ntg * sizeof(LmTarget), hipMemcpyHostToDevice, st) !=
+            hipSuccess) {
+            (void)hipFree(dev_tg);
+            hd_set_error("lora: target list upload failed");
+            return HD_ERR_IO;
+        }
+    }
+    int cus = 0, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    hd_status status = HD_OK;
+    size_t off = 0;
+    auto sb = stream_batches.begin();
+    for (int level = 0; level < nlevels && status == HD_OK; level++) {
+        for (; sb != stream_batches.end() && sb->first.level == level; ++sb) {
+            const int N = sb->first.N, K = sb->first.K, R = sb->first.R;
+            const int ntk = hd_cdiv(K, LT_K), nstrip = hd_cdiv(N, LT_N);
+            const long tot = (long)nstrip * ntk * (long)sb->second.size();
+            if (tot >= ((long)1 << 31)) {
+                hd_set_error("lora: batch of %zu targets has too many tiles", sb->second.size());
+                status = HD_ERR_UNSUPPORTED;
+                break;
+            }
+            lora_merge_stream_kernel<<<tot < cus ? (unsigned)tot : (unsigned)cus, 512, 0, st>>>(
+                dev_tg + off, N, K, R, ntk, nstrip, (int)tot);
+            off += sb->second.size();
+        }
+        for (auto &m : mfma_entries) {
+            if (m.first != level || status != HD_OK) continue;
+            hd_lora_entry *e = &entries[m.second];
+            const int N = (int)e->out_dim, K = (int)e->in_dim, R = (int)e->rank;
+            const float scale = e->multiplier * e->alpha / (float)e->rank;
+            dim3 grid(hd_cdiv(K, LM_T), hd_cdiv(N, LM_T));
             lora_merge_mfma_kernel<2><<<grid, 256, 0, st>>>((uint16_t *)e->base_dev, (const float *)e->up_dev,
                                                             (const float *)e->down_dev, N, K, R, scale);
         }
         hipError_t err = hipGetLastError();
-        if (err != hipSuccess) {
+        if (status == HD_OK && err != hipSuccess) {
             hd_set_error("lora: merge launch failed: %s", hipGetErrorString(err));
-            return HD_ERR_RUNTIME;
+            status = HD_ERR_RUNTIME;
         }
     }
-    return HD_OK;
+    if (dev_tg) {
+        (void)hipStreamSynchronize(st);
+        (void)hipFree(dev_tg);
+    }
+    return status;
 }

@@ -679,6 +679,40 @@ def test_patchify_bf16_and_rotary_scalar_path(pkg, lib, dev):
     assert np.array_equal(host(y), orc.apply_rotary(x, cr, sr, 1))
 
 
+def test_lora_merge_batched_entries_vs_oracle(pkg, lib, dev):
+    """One hd_lora_merge_gpu call over entries of mixed shapes and ranks, as
+    an adapter load makes it: the streaming kernel batches the entries of one
+    (out, in, rank) shape into one launch, the other ranks run the fp32
+    kernel, and two entries on the same weight (two adapters naming one
+    target) merge in entry order, each on the other's result
+    (lora_merge.cu:35-104 loops over the entries in order)."""
+    rng = np.random.default_rng(77)
+    shapes = [(256, 512, 64), (256, 512, 64), (128, 256, 16), (256, 512, 64), (130, 72, 37), (256, 512, 64)]
+    ws = [orc.bf16_round(rng.standard_normal((n, k)).astype(np.float32) * 0.02) for n, k, _ in shapes]
+    wds = [dbf(w, dev) for w in ws]
+    # entry list: every weight once, then weights 1 and 4 a second time
+    order = [0, 1, 2, 3, 4, 5, 1, 4]
+    ents = (pkg.hd_lora_entry * len(order))()
+    keep, refs = [], [w.copy() for w in ws]
+    for j, i in enumerate(order):
+        n, k, r = shapes[i]
+        up = (rng.standard_normal((n, r)) * 0.01).astype(np.float32)
+        down = (rng.standard_normal((r, k)) * 0.01).astype(np.float32)
+        mult = 0.5 + 0.25 * j
+        upd, dnd = torch.from_numpy(up).to(dev), torch.from_numpy(down).to(dev)
+        keep += [upd, dnd]
+        e = ents[j]
+        e.rank, e.in_dim, e.out_dim, e.alpha, e.multiplier = r, k, n, float(r), mult
+        e.down_dev, e.up_dev, e.base_dev = dnd.data_ptr(), upd.data_ptr(), wds[i].data_ptr()
+        refs[i] = orc.lora_merge(refs[i], up, down, mult)
+    assert lib.hd_lora_merge_gpu(ents, len(order), None) == 0
+    torch.cuda.synchronize()
+    for i, (wd, ref) in enumerate(zip(wds, refs)):
+        got = host(wd)
+        assert close_bf16(got, ref, ulps=1, atol_rel=1e-4), i
+        assert np.mean(got == ref) > 0.999, i
+
+
 @pytest.mark.parametrize("N,K,R", [(300, 520, 64), (257, 136, 36), (4224, 1032, 64), (130, 72, 8),
                                    (300, 520, 37), (520, 264, 128)])
 def test_lora_merge_kernels_vs_oracle(pkg, lib, dev, N, K, R):
