@@ -124,7 +124,8 @@ const char *hd_gemm_config_name(int M, int N, int K, int epilogue);
  * k [B,KV,S,128] and the flash V^T layout vt [B,KV,128,S]. cs: rotary table
  * [seq, 64] (cos, sin). Returns 0 when launched, 1 (nothing done) when the
  * shape is outside the fused path: seq % 64 != 0, head counts not even,
- * hidden > 8192 or not a multiple of 64, operands of 2 GiB or more. */
+ * hidden > 8192 or not a multiple of 64, operands of 2 GiB or more, a
+ * pointer (x, norm weights, cs, q, k, vt) not 16-byte aligned. */
 int hd_linear_qkv_rope(const void *x, const void *wq, const void *wk, const void *wv,
                        const void *qn_w, const void *kn_w, const float *cs, void *q, void *k,
                        void *vt, int batch, int seq, int heads, int kv_heads, int hidden,

@@ -46,9 +46,10 @@ struct GemmArgs {
     uint16_t *q_out, *k_out, *vt_out;
     int seq, heads, kv_heads;
     float eps;
-    // tail split (gemm_ms_kernel): blocks < n_whole run whole tiles; the
-    // blocks after them run the K chunks (split per tile) of the last
-    // n_tail tiles and write fp32 partial tiles [BM][BN] to `part`
+    // tail split (gemm_ms_kernel): the first gridDim.x - n_whole blocks run
+    // the K chunks (split per tile) of the last n_tail tiles and write fp32
+    // partial tiles [BM][BN] to `part`; the n_whole blocks after them run
+    // whole tiles
     int n_whole, split;
     float *part;
 };
@@ -143,10 +144,11 @@ template <int CPR> __device__ __forceinline__ int ms_swz(int r) {
 
 // EPI_QKV epilogue for one wave: its WTM rows x 128 columns (one head) are
 // staged in LDS as the bf16 projection output (the reference's rounding
-// point). q/k heads: lane-per-row RMSNorm (the sum of squares uses the
-// pairing and summation tree of the standalone kernels, x_l^2 + x_{l+64}^2
-// then pairs 4, 2, 1 and 32, 16, 8 apart, so results are bit-identical) and rotate-half rotary with
-// bf16 rounding of every product, then coalesced stores to [B,H,S,128].
+// point). q/k heads: RMSNorm with 8 lanes per row (the sum of squares uses
+// the pairing and summation tree of the standalone kernels, x_l^2 +
+// x_{l+64}^2 then pairs 4, 2, 1 and 32, 16, 8 apart, so results are
+// bit-identical) and rotate-half rotary with bf16 rounding of every
+// product, stored straight to [B,H,S,128].
 // v heads: transposed stores into [B,KV,128,S] with key bits 2 and 3
 // exchanged (the flash kernel's V^T layout; S % 64 == 0 so no padding).
 template <int WTM, int LDW>
@@ -154,105 +156,112 @@ __device__ __forceinline__ void qkv_epilogue(const GemmArgs &g, uint16_t *stg, i
                                              int lane) {
     const int H = g.heads, KV = g.kv_heads, S = g.seq;
     if (hslot < H + KV) {
+        // 8 lanes per row, 8 rows per pass: lane j of a row holds columns
+        // 8j .. 8j+7 and their rotary partners 64 + 8j .. 64 + 8j+7, so the
+        // pair sums x_l^2 + x_{l+64}^2 of one lane are one group of 8 of the
+        // summation tree (pairs 4, 2, 1 apart in registers) and the group
+        // sums 32, 16, 8 apart are lanes 4, 2, 1 apart. The rotary table and
+        // the output rows are read and written as 512- and 256-byte runs.
         const uint16_t *w = hslot < H ? g.qn_w : g.kn_w;
-        for (int r = lane; r < WTM; r += 64) {
-            const int m = gm0 + r;
-            if (m >= g.M) break;
-            uint16_t *row = stg + r * LDW;
-            float v[64];
+        const int j = lane & 7;
+        const u32x4_t wlo = *(const u32x4_t *)(w + j * 8), whi = *(const u32x4_t *)(w + 64 + j * 8);
+        const int hx = hslot < H ? hslot : hslot - H, nh = hslot < H ? H : KV;
+        uint16_t *base = hslot < H ? g.q_out : g.k_out;
+        // two passes at a time: their staged rows and rotary rows are
+        // requested before any of them is used
+        constexpr int NP8 = WTM / 8;
+        constexpr int NPASS = NP8 % 2 == 0 ? 2 : 1;
+        static_assert(WTM % (8 * NPASS) == 0, "q/k epilogue passes");
+        for (int rb = 0; rb < WTM; rb += 8 * NPASS) {
+            u32x4_t lo[NPASS], hi[NPASS];
+            float4 csv[NPASS][4];
 #pragma unroll
-            for (int c = 0; c < 8; c++) {
-                const u32x4_t lo = *(const u32x4_t *)(row + c * 8);
-                const u32x4_t hi = *(const u32x4_t *)(row + 64 + c * 8);
+            for (int p = 0; p < NPASS; p++) {
+                const int r = rb + p * 8 + (lane >> 3);
+                const uint16_t *row = stg + r * LDW;
+                lo[p] = *(const u32x4_t *)(row + j * 8);
+                hi[p] = *(const u32x4_t *)(row + 64 + j * 8);
+                const int s = (gm0 + r) % S;
+                const float4 *cs4 = (const float4 *)(g.cs + (size_t)s * 64 + j * 8);
+#pragma unroll
+                for (int c = 0; c < 4; c++) csv[p][c] = cs4[c];
+            }
+#pragma unroll
+            for (int p = 0; p < NPASS; p++) {
+                const int m = gm0 + rb + p * 8 + (lane >> 3);
+                float v[8];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const float a0 = lo_bf(lo[e]), a1 = hi_bf(lo[e]);
-                    const float b0 = lo_bf(hi[e]), b1 = hi_bf(hi[e]);
-                    v[c * 8 + 2 * e] = fmaf(a0, a0, b0 * b0);
-                    v[c * 8 + 2 * e + 1] = fmaf(a1, a1, b1 * b1);
+                    const float a0 = lo_bf(lo[p][e]), a1 = hi_bf(lo[p][e]);
+                    const float b0 = lo_bf(hi[p][e]), b1 = hi_bf(hi[p][e]);
+                    v[2 * e] = fmaf(a0, a0, b0 * b0);
+                    v[2 * e + 1] = fmaf(a1, a1, b1 * b1);
                 }
-            }
-            // the q/k norm's summation tree (shared by every q/k norm
-            // kernel): pairs 4, 2, 1 apart inside each group of 8, then the
-            // group sums 32, 16, 8 apart
 #pragma unroll
-            for (int o = 4; o > 0; o >>= 1)
+                for (int o = 4; o > 0; o >>= 1)
 #pragma unroll
-                for (int k = 0; k < 64; k++)
-                    if ((k & 7) < o) v[k] = v[k] + v[k + o];
-#pragma unroll
-            for (int o = 32; o >= 8; o >>= 1)
-#pragma unroll
-                for (int k = 0; k < o; k += 8) v[k] = v[k] + v[k + o];
-            const float inv = 1.0f / sqrtf(v[0] / 128.0f + g.eps);
-            const int s = m % S;
-            const float2 *cs = g.cs + (size_t)s * 64;
-#pragma unroll 4
-            for (int c = 0; c < 8; c++) {
-                const u32x4_t lo = *(const u32x4_t *)(row + c * 8);
-                const u32x4_t hi = *(const u32x4_t *)(row + 64 + c * 8);
+                    for (int k = 0; k < o; k++) v[k] = v[k] + v[k + o];
+                float ss = v[0];
+                ss = ss + __shfl_xor(ss, 4, 64);
+                ss = ss + __shfl_xor(ss, 2, 64);
+                ss = ss + __shfl_xor(ss, 1, 64);
+                if (m >= g.M) continue;
+                const float inv = 1.0f / sqrtf(ss / 128.0f + g.eps);
+                const int b = m / S, s = m % S;
                 u32x4_t olo, ohi;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     float o0[2], o1[2];
 #pragma unroll
                     for (int t = 0; t < 2; t++) {
-                        const int l = c * 8 + 2 * e + t;
-                        const float x0 = t ? hi_bf(lo[e]) : lo_bf(lo[e]);
-                        const float x1 = t ? hi_bf(hi[e]) : lo_bf(hi[e]);
-                        const float y0 = bfround(bf2f(w[l]) * x0 * inv);
-                        const float y1 = bfround(bf2f(w[l + 64]) * x1 * inv);
-                        const float2 r2 = cs[l];
-                        o0[t] = bfround(y0 * r2.x) - bfround(y1 * r2.y);
-                        o1[t] = bfround(y1 * r2.x) + bfround(y0 * r2.y);
+                        const float x0 = t ? hi_bf(lo[p][e]) : lo_bf(lo[p][e]);
+                        const float x1 = t ? hi_bf(hi[p][e]) : lo_bf(hi[p][e]);
+                        const float w0 = t ? hi_bf(wlo[e]) : lo_bf(wlo[e]);
+                        const float w1 = t ? hi_bf(whi[e]) : lo_bf(whi[e]);
+                        const float y0 = bfround(w0 * x0 * inv);
+                        const float y1 = bfround(w1 * x1 * inv);
+                        const float4 c4 = csv[p][e];
+                        const float cr = t ? c4.z : c4.x, sr = t ? c4.w : c4.y;
+                        o0[t] = bfround(y0 * cr) - bfround(y1 * sr);
+                        o1[t] = bfround(y1 * cr) + bfround(y0 * sr);
                     }
                     olo[e] = pack_bf2(o0[0], o0[1]);
                     ohi[e] = pack_bf2(o1[0], o1[1]);
                 }
-                *(u32x4_t *)(row + c * 8) = olo;
-                *(u32x4_t *)(row + 64 + c * 8) = ohi;
-            }
-        }
-        // rows were rewritten by their own lanes; the store pass reads
-        // other lanes' rows of this wave's staging area
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const int hx = hslot < H ? hslot : hslot - H, nh = hslot < H ? H : KV;
-        uint16_t *base = hslot < H ? g.q_out : g.k_out;
-#pragma unroll 4
-        for (int r0 = 0; r0 < WTM; r0 += 4) {
-            const int r = r0 + lane / 16, cc = (lane % 16) * 8;
-            const int m = gm0 + r;
-            if (m < g.M) {
-                const int b = m / S, s = m % S;
-                *(u32x4_t *)(base + (((size_t)b * nh + hx) * S + s) * 128 + cc) =
-                    *(const u32x4_t *)(stg + r * LDW + cc);
+                uint16_t *orow = base + (((size_t)b * nh + hx) * S + s) * 128;
+                *(u32x4_t *)(orow + j * 8) = olo;
+                *(u32x4_t *)(orow + 64 + j * 8) = ohi;
             }
         }
     } else {
         const int hk = hslot - H - KV;
-        // lane: d = d0 + lane / 16, 8 storage columns (half of a 16-key group)
-        for (int d0 = 0; d0 < 128; d0 += 4) {
-            const int d = d0 + lane / 16, c = lane % 16;
+        // 8 keys x 8 dimensions per lane and item: 8 16-byte row reads (the
+        // item's keys, dimensions 8*lane%16 .. +7), a register transpose, 8
+        // 16-byte stores (one per dimension: the 8 storage columns of one
+        // half of a 16-key group). Items: (16-key group, half), 4 per pass.
+        const int dblk = lane & 15;
+        constexpr int NITEM = WTM / 8;
+        for (int it = lane >> 4; it < NITEM; it += 4) {
+            const int grp = it >> 1, half = it & 1;
+            const int m = gm0 + grp * 16;
+            u32x4_t rw[8];
 #pragma unroll
-            for (int gq = 0; gq < WTM / 128 + (WTM % 128 ? 1 : 0); gq++) {
-                const int grp = gq * 8 + c / 2, half = c % 2;   // 16-key group within the wave
-                if (grp * 16 >= WTM) continue;
-                const int m = gm0 + grp * 16;
-                if (m >= g.M) continue;
-                const int b = m / S, s = m % S;
-                uint16_t vals[8];
+            for (int e = 0; e < 8; e++) {
+                const int p = half * 8 + e;                                   // storage column in the group
+                const int src = (p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1);  // key at that column
+                rw[e] = *(const u32x4_t *)(stg + (grp * 16 + src) * LDW + dblk * 8);
+            }
+            if (m >= g.M) continue;
+            const int b = m / S, s = m % S;
+            uint16_t *dst = g.vt_out + (((size_t)b * KV + hk) * 128 + dblk * 8) * S + s + half * 8;
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const int p = half * 8 + e;                                   // storage column in the group
-                    const int src = (p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1);  // key at that column
-                    vals[e] = stg[(grp * 16 + src) * LDW + d];
-                }
+            for (int dd = 0; dd < 8; dd++) {
+                const uint32_t sel = dd & 1 ? 0x07060302u : 0x05040100u;
                 u32x4_t pk;
 #pragma unroll
-                for (int e = 0; e < 4; e++) pk[e] = (uint32_t)vals[2 * e] | ((uint32_t)vals[2 * e + 1] << 16);
-                *(u32x4_t *)(g.vt_out + (((size_t)b * KV + hk) * 128 + d) * S + s + half * 8) = pk;
+                for (int w = 0; w < 4; w++)
+                    pk[w] = __builtin_amdgcn_perm(rw[2 * w + 1][dd >> 1], rw[2 * w][dd >> 1], sel);
+                *(u32x4_t *)(dst + (size_t)dd * S) = pk;
             }
         }
     }
@@ -286,13 +295,18 @@ __global__ __launch_bounds__(WGM * WGN * 64, OCC) void gemm_ms_kernel(GemmArgs g
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
-    // whole tiles first (XCD-contiguous over them), then the K chunks of the
-    // tail tiles (lin >= n_whole), `split` consecutive blocks per tile
+    // the K chunks of the tail tiles (lin >= n_whole, `split` consecutive
+    // blocks per tile) first, then the whole tiles (XCD-contiguous over
+    // them). The CUs that start with a chunk run their whole tiles offset
+    // from the others, so a round's epilogues (output stores, residual
+    // reads) do not all reach HBM at once: +2-3 % for the residual GEMMs
+    // at 4-6 rounds, equal elsewhere.
     int lin, chunk = -1, item = 0;
-    if ((int)blockIdx.x < g.n_whole) {
-        lin = xcd_remap(blockIdx.x, g.n_whole);
+    const int n_chunks = (int)gridDim.x - g.n_whole;
+    if ((int)blockIdx.x >= n_chunks) {
+        lin = xcd_remap(blockIdx.x - n_chunks, g.n_whole);
     } else {
-        item = blockIdx.x - g.n_whole;
+        item = blockIdx.x;
         chunk = item % g.split;
         lin = g.n_whole + item / g.split;
     }
@@ -982,7 +996,8 @@ extern "C" int hd_linear_qkv_rope_ws(const void *x, const void *wq, const void *
                     (kv_heads * 128) % 256 == 0 && hidden % 64 == 0 && hidden <= 8192 &&
                     (size_t)(M + 256) * hidden * 2 < ((size_t)1 << 31) &&
                     (size_t)heads * 128 * hidden * 2 < ((size_t)1 << 31) &&
-                    ((uintptr_t)x % 16 == 0) && ((uintptr_t)vt % 16 == 0);
+                    ((((uintptr_t)x | (uintptr_t)vt | (uintptr_t)q | (uintptr_t)k | (uintptr_t)qn_w |
+                       (uintptr_t)kn_w | (uintptr_t)cs) & 15) == 0);
     if (!ok) return 1;
     GemmArgs g = {};
     g.A = (const uint16_t *)x;
