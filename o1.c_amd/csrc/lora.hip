@@ -162,10 +162,12 @@ __device__ __forceinline__ void split3(float x, uint16_t &h0, uint16_t &h1, uint
 //    the accumulator layout, writes the bf16 result back in place, and the
 //    tile leaves with coalesced 16-byte buffer stores;
 //  - the rank product uses the three-part split above (six bf16 part
-//    products per fp32 product, in three accumulators); the up strip's part planes
-//    are staged once per row strip, the down slice's once per tile, into one
-//    of two plane buffers, from registers loaded a tile ahead, while the
-//    previous tile's MFMAs run (two barriers per tile);
+//    products per fp32 product, in three accumulators); the up strip's part
+//    planes are staged once per row strip and each wave keeps its B
+//    fragments of them in registers for the whole strip; the down slice's
+//    planes are staged once per tile, into one of two plane buffers, from
+//    registers loaded a tile ahead, while the tile's MFMAs run (all twelve A
+//    fragments of a tile are requested before its first MFMA);
 //  - MFMA A = down^T (rows: W columns k), B = up (columns: W rows n), so a
 //    lane holds four consecutive k of one W row per accumulator group.
 // Every vector memory instruction in the loop is issued unconditionally
@@ -333,6 +335,17 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(const LmTarge
     int staged = c0.g * nstrip + c0.tn;   // target and row strip of the staged up planes
     stage_up(c0);          // vmcnt(0): down(tb) landed as well
     put_down(DA, tb & 1);
+    // this wave's up fragments (B operands) stay in registers for the whole
+    // row strip: read from the staged planes after each staging barrier
+    bf16x8_t fb[4][3];
+    auto read_up = [&]() {
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+            for (int p = 0; p < 3; p++)
+                fb[ks][p] = *(const bf16x8_t *)(upl[p] + (nblk * 32 + l32) * LT_LD + ks * 16 + lh * 8);
+    };
+    bool need_up = true;
     // tile t splits down(t+1) (registers dsplit) for the next tile and loads
     // down(t+2) into the registers down(t) used (dload); the loop runs two
     // tiles per trip with the two register sets swapped, so no register
@@ -345,6 +358,11 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(const LmTarge
             stage_up(c0);
             staged = c0.g * nstrip + c0.tn;
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            need_up = true;
+        }
+        if (need_up) {
+            read_up();
+            need_up = false;
         }
         // the MFMAs of tile t; the next tile's down slice is split into the
         // other plane buffer in between (independent VALU and LDS work)
@@ -355,23 +373,28 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(const LmTarge
         f32x16_t acc_s, acc_m, acc_l;
 #pragma unroll
         for (int e = 0; e < 16; e++) acc_s[e] = acc_m[e] = acc_l[e] = 0.f;
+        // every fragment of the tile is requested before the first MFMA
+        bf16x8_t fa[4][3];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             const int rc = ks * 16 + lh * 8;
-            bf16x8_t a[3], bb[3];
 #pragma unroll
-            for (int p = 0; p < 3; p++) {
-                a[p] = *(const bf16x8_t *)(dpl[b][p] + (kblk * 32 + l32) * LT_LD + rc);
-                bb[p] = *(const bf16x8_t *)(upl[p] + (nblk * 32 + l32) * LT_LD + rc);
-            }
+            for (int p = 0; p < 3; p++)
+                fa[ks][p] = *(const bf16x8_t *)(dpl[b][p] + (kblk * 32 + l32) * LT_LD + rc);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const bf16x8_t *a = fa[ks], *bb = fb[ks];
             acc_s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], bb[0], acc_s, 0, 0, 0);
             acc_m = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], bb[0], acc_m, 0, 0, 0);
             acc_l = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], bb[0], acc_l, 0, 0, 0);
             acc_s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], bb[1], acc_s, 0, 0, 0);
             acc_m = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], bb[1], acc_m, 0, 0, 0);
             acc_s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], bb[2], acc_s, 0, 0, 0);
-            if (ks == 1) put_down(dsplit, b ^ 1);
         }
+        // the next tile's down slice into the other plane buffer (its reads
+        // above are issued; the MFMAs run meanwhile)
+        put_down(dsplit, b ^ 1);
         f32x16_t acc;
 #pragma unroll
         for (int e = 0; e < 16; e++) acc[e] = acc_l[e] + (acc_m[e] + acc_s[e]);
@@ -416,12 +439,16 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(const LmTarge
         }
         // the sub-tile leaves as it arrived (same lanes, same offsets)
         const __amdgpu_buffer_rsrc_t rw = lt_rsrc(c0.w, w_bytes);
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const uint32_t sa = (uint32_t)(size_t)(HD_LDS void *)(sub + (i * 64 + lane) * 8);
-            u32x4_t v;
-            asm volatile("s_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(sa) : "memory");
-            __builtin_amdgcn_raw_buffer_store_b128(v, rw, w_off(c0, i), 0, 0);
+        {
+            // LDS operations of one wave complete in order, so these reads
+            // see the update's writes above
+            const uint32_t sa0 = (uint32_t)(size_t)(HD_LDS void *)(sub + lane * 8);
+            const uint32_t sa1 = (uint32_t)(size_t)(HD_LDS void *)(sub + (64 + lane) * 8);
+            u32x4_t v0, v1;
+            asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+                         : "=v"(v0), "=v"(v1) : "v"(sa0), "v"(sa1) : "memory");
+            __builtin_amdgcn_raw_buffer_store_b128(v0, rw, w_off(c0, 0), 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(v1, rw, w_off(c0, 1), 0, 0);
         }
         c0 = c1;
         c1 = c2;
