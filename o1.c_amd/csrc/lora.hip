@@ -405,8 +405,10 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(const LmTarge
         load_down(c2, dload);
         // W update in LDS, in this wave's own sub-tile: row l32, columns
         // 8q + 4lh .. +3 (chunk q at position q ^ ((l32 >> 2) & 3)). W(t) of
-        // this wave landed: newer than it are down(t), the stores of t-2,
-        // W(t+1), down(t+1), the stores of t-1, W(t+2) and down(t+2) (14; on
+        // this wave landed: newer than it are the loads down(t), W(t+1),
+        // down(t+1), W(t+2) and down(t+2) (10) and the stores of t-2 and t-1
+        // (4). The count allows only the 10 newer loads in flight, so it
+        // holds even if the stores complete before older loads return (on
         // the first tiles a full drain came since). The ring is touched
         // through assembly only: the compiler would otherwise wait for every
         // buffer->LDS load in flight (vmcnt(0)) before each access.
@@ -418,7 +420,7 @@ __global__ __launch_bounds__(512, 1) void lora_merge_stream_kernel(const LmTarge
                 ad[q] = (uint32_t)(size_t)(HD_LDS void *)(sub + (l32 * 4 + (q ^ ((l32 >> 2) & 3))) * 8 + lh * 4);
             u32x2_t wv[4];
             asm volatile(
-                "s_waitcnt vmcnt(12)\n\t"
+                "s_waitcnt vmcnt(10)\n\t"
                 "ds_read_b64 %0, %4\n\tds_read_b64 %1, %5\n\tds_read_b64 %2, %6\n\tds_read_b64 %3, %7\n\t"
                 "s_waitcnt lgkmcnt(0)"
                 : "=v"(wv[0]), "=v"(wv[1]), "=v"(wv[2]), "=v"(wv[3])
